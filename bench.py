@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""All-points FRNN (grid build + neighbour search) on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config metric|C1..C5] [--no-cpu]
+
+A step is one FRNNEngine.search_gpu call (reference: frnn_engine.cu:195-250)
+over the configuration's synthetic cloud, with the SoA input already resident
+in HBM and the outputs left in HBM -- the timing the reference's harness uses
+(Tests/scripts/benchmark_vs_libfrnn.py:146-169).  Prints ONE JSON line on stdout:
+
+  value            mean ms per step over exactly K steps (sync before and after)
+  roofline         dominant kernel (the neighbour search): algorithmic fp32 flops
+                   (2*D per shell candidate pair) / its mean HIP-event duration,
+                   against the fp32 MFMA peak; traffic from the committed
+                   rocprofv3 PMC summary when present
+  build_hbm        grid-build kernels: algorithmic bytes / event time vs 8 TB/s
+  cpu_baseline     the C++/OpenMP restatement (oracle/) on a bounded query sample,
+                   timed on this host, extrapolated to all N queries; the same
+                   sample is also compared bit-exactly with the GPU rows
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "pure_cuda-c-_frnn_amd"), os.path.join(ROOT, "oracle")]
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F32_PEAK_TFLOPS = 157.3
+METRIC = "ms per all-points FRNN (build+search) + HBM GB/s frac, D=16 N=1M K=64"
+
+
+def eprint(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_bytes(N, D, ds, g, C):
+    """Algorithmic HBM bytes of each build kernel (4-byte ints and floats); ds is
+    the padded AoS row length the reorder writes."""
+    return {
+        "zero_fill": 4 * (C + 1),
+        "bin_count": 4 * g * N + 8 * N + 8 * (C + 1),
+        "scan": 8 * (C + 1),
+        "reorder": 20 * N + 4 * D * N + 4 * ds * N,
+    }
+
+
+def traffic_from_profiles(config):
+    path = os.path.join(ROOT, "profiles", f"search_pmc_{config}.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        p = json.load(f)
+    return p.get("hbm_bytes_per_dispatch"), os.path.relpath(path, ROOT)
+
+
+def cpu_baseline(w, gi, gd, target_s, threads):
+    import frnn_oracle as O
+    rs = np.random.RandomState(99)
+    # calibration run on a small sample, then one run sized to ~target_s of search work
+    q0 = min(w.N, 1000)
+    t = []
+    O.search(w.X, w.K, w.radius, nthreads=threads,
+             query_ids=np.sort(rs.choice(w.N, q0, replace=False)).astype(np.int32), timings=t)
+    per_q = max(t[1] / q0, 1e-9)
+    nq = int(min(w.N, max(q0, target_s / per_q)))
+    q = np.sort(rs.choice(w.N, nq, replace=False)).astype(np.int32)
+    t = []
+    ri, rd = O.search(w.X, w.K, w.radius, nthreads=threads, query_ids=q, timings=t)
+    build_s, search_s = t
+    full_ms = 1e3 * (build_s + search_s * w.N / nq)
+    same = np.all(gi[q] == ri, 1) & np.all(gd[q].view(np.uint32) == rd.view(np.uint32), 1)
+    return {
+        "value": round(full_ms, 3), "unit": "ms", "cores": threads, "kind": "port",
+        "sample": f"{nq} of {w.N} queries (random, seed 99) against the full database, with the "
+                  f"full grid build; search time scaled by N/{nq}: build {build_s * 1e3:.1f} ms + "
+                  f"search {search_s:.2f} s",
+        "speedup_vs_gpu": None, "parity_sample_rows": nq,
+        "parity_mismatched_rows": int(np.sum(~same)),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="metric")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        eprint(f"bench.py: --gpus {args.gpus} (WORLD_SIZE={world}) requested, but this engine runs on "
+               f"one GPU only; there is no multi-GPU path to measure. Run with --gpus 1.")
+        sys.exit(2)
+
+    import torch
+    import frnn_cuda
+    import frnn_workloads as W
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    t_gen = time.perf_counter()
+    w = W.config(args.config)
+    eprint(f"[bench] {w.name}: N={w.N} D={w.D} K={w.K} r={w.radius:.6f} "
+           f"(data {time.perf_counter() - t_gen:.1f}s)")
+    plan = frnn_cuda.plan(w.N, w.D, w.K, w.radius)
+    d = torch.from_numpy(w.soa()).to("cuda:0")
+    torch.cuda.synchronize()
+    eng = frnn_cuda.FRNNEngine(max_points=w.N)
+    ptr = d.data_ptr()
+    for _ in range(args.warmup):
+        eng.search_gpu(ptr, w.N, w.D, w.K, w.radius)
+    eprint(f"[bench] warmup done ({args.warmup} steps), path={plan['path']}")
+
+    eng.set_profiling(True)      # HIP events around every kernel of each timed step
+    stage_sum = {}
+    steps_ms = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        s0 = time.perf_counter()
+        eng.search_gpu(ptr, w.N, w.D, w.K, w.radius)   # synchronous
+        steps_ms.append((time.perf_counter() - s0) * 1e3)
+        for k, v in eng.stage_times().items():
+            stage_sum[k] = stage_sum.get(k, 0.0) + v
+    torch.cuda.synchronize()
+    total_s = time.perf_counter() - t0
+    ctr = eng.counters()
+    eng.set_profiling(False)
+    ms_per_step = total_s * 1e3 / args.steps
+    stages = {k: v / args.steps for k, v in stage_sum.items()}
+    eprint(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step; stages " +
+           ", ".join(f"{k}={v:.3f}" for k, v in stages.items()))
+
+    idx, dist = eng.get_results_numpy(w.N, w.K)
+    gi = idx.reshape(w.K, w.N).T
+    gd = dist.reshape(w.K, w.N).T
+
+    # dominant kernel roofline: fp32 MFMA
+    pairs = ctr["shell_candidates"]
+    flops = 2.0 * w.D * pairs
+    search_s = stages["search"] / 1e3
+    achieved = flops / search_s / 1e12
+    traffic, traffic_src = traffic_from_profiles(args.config)
+    roofline = {"kernel": "search_kernel (neighbour search)", "bound": "mfma",
+                "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4), "traffic": traffic,
+                "flops_per_launch": flops, "shell_candidate_pairs": pairs,
+                "mean_kernel_ms": round(stages["search"], 4),
+                "traffic_source": traffic_src}
+
+    bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"], plan["cells"]) if plan["path"] != "bruteforce" else {}
+    build = {}
+    tot_b, tot_ms = 0, 0.0
+    for k, b in bb.items():
+        ms = stages[k]
+        gbs = b / (ms / 1e3) / 1e9 if ms > 0 else 0.0
+        build[k] = {"bytes": b, "ms": round(ms, 4), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        tot_b += b
+        tot_ms += ms
+    if tot_ms > 0:
+        g = tot_b / (tot_ms / 1e3) / 1e9
+        build["total"] = {"bytes": tot_b, "ms": round(tot_ms, 4), "GBps": round(g, 1),
+                          "frac": round(g / HBM_PEAK_GBS, 4)}
+    end_to_end_bytes = tot_b + 8 * w.D * w.N + 16 * w.K * w.N
+    e2e_gbs = end_to_end_bytes / (ms_per_step / 1e3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        eprint(f"[bench] cpu baseline with {threads} threads (~{args.cpu_seconds:.0f}s sample)")
+        cpu = cpu_baseline(w, gi, gd, args.cpu_seconds, threads)
+        cpu["speedup_vs_gpu"] = round(cpu["value"] / ms_per_step, 1)
+        eprint(f"[bench] cpu {cpu['value']:.1f} ms (x{cpu['speedup_vs_gpu']}), parity mismatched rows "
+               f"{cpu['parity_mismatched_rows']}/{cpu['parity_sample_rows']}")
+
+    line = {
+        "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "ms_median": round(float(np.median(steps_ms)), 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (numpy RandomState 1234, recipe in frnn_workloads.py)",
+        "config": {"workload": w.name, "N": w.N, "D": w.D, "K": w.K, "radius": w.radius,
+                   "raw_radius": w.notes.get("raw_radius"), "path": plan["path"],
+                   "grid_dim": plan["grid_dim"], "res": plan["res"], "cells": plan["cells"],
+                   "queries_per_s": round(w.N / (ms_per_step / 1e3), 1)},
+        "roofline": roofline,
+        "build_hbm": build,
+        "end_to_end_hbm": {"bytes": end_to_end_bytes, "GBps": round(e2e_gbs, 1),
+                           "frac": round(e2e_gbs / HBM_PEAK_GBS, 5)},
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+        "counters": ctr,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    eng.close()
+
+
+if __name__ == "__main__":
+    main()

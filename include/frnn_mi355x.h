@@ -1,0 +1,176 @@
+/*
+ * frnn_mi355x.h -- C ABI of the MI355X (gfx950) fixed-radius nearest-neighbour engine.
+ *
+ * Plain C types only: device pointers are raw addresses, streams are hipStream_t
+ * passed as void*.  Every entry point returns an frnn_status (0 = success) and
+ * validates its arguments on the host before any HIP call.
+ *
+ * Reference interfaces replaced (paths under the reference tree):
+ *   engine entry points    python_interface/frnn_engine.h:9-55 and
+ *                          python_interface/nanobind_module.cu:8-21 (FRNNEngine)
+ *   kernel launch seam     python_interface/frnn_engine.cu:9-20 (extern "C" run_*)
+ *
+ * Layouts (same as the reference):
+ *   input   SoA fp32, p[d*N + i]                       (frnn_engine.h:21-26)
+ *   output  SoA, idx[k*N + i] int32, dist[k*N + i] fp32 squared L2
+ *                                                      (find_nbrs.cu:206-213)
+ * Semantics: every point is a query; the neighbours of query i are the (up to)
+ * K points j with fl32 squared distance d2 < fl32(radius*radius), the K
+ * smallest in (d2, j) order, written in ascending order; unused slots hold
+ * (d2 = r2, idx = -1).
+ */
+#ifndef FRNN_MI355X_H
+#define FRNN_MI355X_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FRNN_MAX_K 128           /* grid.h:59 MAX_K_CAPACITY */
+#define FRNN_MAX_DIM 128         /* grid.h:60 MAX_DIM_SUPPORTED */
+#define FRNN_MAX_CELLS 1000000   /* frnn_engine.cu:35 */
+
+enum frnn_status {
+    FRNN_OK = 0,
+    FRNN_ERR_INVALID_ARGUMENT = 1, /* N, dim, K, radius or a pointer out of range */
+    FRNN_ERR_CAPACITY = 2,         /* N above the engine's max_points, or sizes too large */
+    FRNN_ERR_HIP = 3,              /* a HIP runtime call or kernel launch failed */
+    FRNN_ERR_NO_DEVICE = 4,        /* no HIP device visible */
+    FRNN_ERR_STATE = 5             /* e.g. get_results before any search */
+};
+
+enum frnn_path {
+    FRNN_PATH_EMPTY = -1,          /* N == 0: nothing to do */
+    FRNN_PATH_BRUTEFORCE = 0,      /* frnn_engine.cu:224-225 / :156,228 fallback */
+    FRNN_PATH_GRID_FULL = 1,       /* full-D uniform grid, frnn_engine.cu:230-245 */
+    FRNN_PATH_GRID_FIRST = 2       /* first-coordinate grid, frnn_engine.cu:64-102 */
+};
+
+/* Result of the reference's auto-dispatch (frnn_engine.cu:201-246, :64-86). */
+typedef struct frnn_plan {
+    int path;          /* enum frnn_path */
+    int grid_dim;      /* g: number of gridded coordinates (0 for brute force) */
+    int res;           /* cells per gridded axis */
+    int rev_order;     /* 1: D=3 grid distance order fma(dx,dx,fma(dy,dy,dz*dz)) */
+    long long cells;   /* res^g */
+    float r2;          /* fl32(radius * radius) */
+    float cell_size;   /* cell edge = radius (frnn_engine.cu:206) */
+    float inv_cell;    /* fl32(1 / radius) */
+} frnn_plan_t;
+
+typedef struct frnn_engine frnn_engine_t;
+
+/* ---- host-only helpers (no HIP call) ------------------------------------ */
+
+const char* frnn_status_string(int status);
+/* Message of the last failure on the calling thread ("" if none). */
+const char* frnn_last_error(void);
+int frnn_version(void);
+
+/* Argument checks the reference never made (grid.h:59-60 documents K, D <= 128;
+ * C9 of the reference contract): 0 < N <= max_points, 1 <= dim <= 128,
+ * 1 <= K <= 128, radius finite and > 0.  max_points <= 0 skips the N check. */
+int frnn_validate(int max_points, int N, int dim, int K, float radius);
+
+/* The reference dispatch rules, integer-exact (frnn_engine.cu:201-246, :64-86). */
+int frnn_make_plan(int N, int dim, int K, float radius, frnn_plan_t* out);
+
+/* Workspace geometry used by the launch seam below. */
+int frnn_aos_stride(int dim);                 /* padded AoS row length in floats */
+int frnn_list_capacity(int K);                /* per-query candidate list entries */
+int frnn_scan_partials_count(int n);          /* ints of scratch for frnn_launch_exclusive_scan */
+
+/* ---- engine (replaces FRNNEngine, frnn_engine.h:9-55) -------------------- */
+
+/* FRNNEngine::FRNNEngine(int max_points), frnn_engine.cu:23-46 */
+int frnn_engine_create(int max_points, frnn_engine_t** out);
+/* FRNNEngine::~FRNNEngine, frnn_engine.cu:48-55 */
+int frnn_engine_destroy(frnn_engine_t* engine);
+int frnn_engine_max_points(const frnn_engine_t* engine, int* out);
+
+/* FRNNEngine::search_gpu, frnn_engine.cu:195-250.  d_points_soa is borrowed for
+ * the call; *d_idxs / *d_dists receive engine-owned device buffers (SoA
+ * [k*N+i]) valid until the next search or destroy.  Synchronous. */
+int frnn_engine_search_gpu(frnn_engine_t* engine, const float* d_points_soa, int N, int dim,
+                           int K, float radius, int** d_idxs, float** d_dists);
+
+/* FRNNEngine::search, frnn_engine.cu:104-193.  Host AoS points [i*dim + d] with
+ * n_values = max_points * dim; N is max_points as in the reference
+ * (frnn_engine.cu:108-109).  Outputs are host AoS [i*K + k], n_values/dim*K each. */
+int frnn_engine_search(frnn_engine_t* engine, const float* h_points_aos, long long n_values,
+                       int K, float radius, int* h_idxs_aos, float* h_dists_aos);
+
+/* FRNNEngine::get_results, frnn_engine.cu:252-258: copies N*K entries of the
+ * last search_gpu output device->host, SoA order [k*N+i], no un-transpose. */
+int frnn_engine_get_results(frnn_engine_t* engine, int N, int K, int* h_idxs_soa,
+                            float* h_dists_soa);
+
+/* Stream for all engine work (default: the null stream, as the reference). */
+int frnn_engine_set_stream(frnn_engine_t* engine, void* hip_stream);
+
+/* Plan used by the last search. */
+int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
+
+/* Per-stage HIP event timing (replaces the reference's FRNN_REPORT_OCCUPANCY
+ * diagnostics, find_nbrs.cu:355-382).  Stages: 0 zero-fill, 1 bin+count,
+ * 2 scan, 3 reorder/transpose, 4 neighbour search, 5 unpermute. */
+#define FRNN_NUM_STAGES 6
+int frnn_engine_set_profiling(frnn_engine_t* engine, int enable);
+int frnn_engine_stage_times(const frnn_engine_t* engine, float* ms, int n);
+/* Work counters of the last profiled search: [0] shell candidates (sum over
+ * queries of the points in their 3^g cells, or N per query for brute force),
+ * [1] pairs passing the MFMA filter, [2] pairs accepted after the exact check.
+ * A profiled search also fails with FRNN_ERR_HIP if the kernel's internal
+ * capacity guards ever fired. */
+#define FRNN_NUM_COUNTERS 3
+int frnn_engine_counters(const frnn_engine_t* engine, long long* out, int n);
+
+/* ---- kernel launch seam (replaces run_*, frnn_engine.cu:9-20) ------------ */
+/* All pointers are device pointers; launches are asynchronous on `stream`. */
+
+/* run_insert_points (insert_points.cu:45-88,167-174): zero d_cnt[0..cells],
+ * bin every point on the first grid_dim coordinates (clamped to [0,res-1]),
+ * d_cell_of[i] = row-major cell id, d_rank[i] = arrival slot in its cell,
+ * d_cnt[c] = occupancy. */
+int frnn_launch_bin_count(const float* d_points_soa, int N, int grid_dim, int res,
+                          float inv_cell, long long cells, int* d_cell_of, int* d_rank,
+                          int* d_cnt, void* stream);
+
+/* thrust::exclusive_scan (frnn_engine.cu:91-94): d_out[i] = sum_{j<i} d_in[j]
+ * for i < n.  d_partials holds frnn_scan_partials_count(n) ints. */
+int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partials,
+                               void* stream);
+
+/* run_counting_sort / run_counting_sort_aos3 (insert_points.cu:142-164,205-226):
+ * pos = d_start[cell] + rank; d_sorted_idx[pos] = i; d_inv[i] = pos; AoS row
+ * pos of d_sorted_aos (stride frnn_aos_stride(dim), zero padded) = point i. */
+int frnn_launch_reorder(const float* d_points_soa, int N, int dim, const int* d_cell_of,
+                        const int* d_rank, const int* d_start, int* d_sorted_idx, int* d_inv,
+                        float* d_sorted_aos, void* stream);
+
+/* Brute-force input staging: AoS copy of the SoA points in original order. */
+int frnn_launch_transpose(const float* d_points_soa, int N, int dim, float* d_aos, void* stream);
+
+/* run_find_nbrs / run_find_nbrs_griddim / run_find_nbrs_aos3 / run_bruteforce
+ * (find_nbrs.cu:525-633, no_grid_frnn.cu:273-326): neighbour search over the
+ * plan's path.  Grid paths read the cell-sorted AoS points, d_sorted_idx and
+ * d_start (cells+1 exclusive offsets); brute force reads the transposed AoS
+ * points and ignores both.  Results: for sorted position s, entries
+ * d_lists[s*list_cap + k], k < K, hold ascending keys (bits(d2) << 32 | idx)
+ * with padding (bits(r2) << 32 | 0xffffffff).  d_counters (3 u64, may be NULL)
+ * accumulates the work counters. */
+int frnn_launch_find_nbrs(const float* d_aos, const int* d_sorted_idx, const int* d_start,
+                          int N, int dim, int K, const frnn_plan_t* plan,
+                          unsigned long long* d_lists, int list_cap,
+                          unsigned long long* d_counters, void* stream);
+
+/* run_scatter_to_orig (find_nbrs.cu:505-535): output row of original query i is
+ * list row d_inv[i] (identity when d_inv is NULL); writes SoA [k*N+i]. */
+int frnn_launch_unpermute(const unsigned long long* d_lists, int list_cap, const int* d_inv,
+                          int N, int K, int* d_idxs, float* d_dists, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRNN_MI355X_H */

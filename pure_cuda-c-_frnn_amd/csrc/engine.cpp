@@ -1,0 +1,500 @@
+// engine.cpp -- host side of the MI355X FRNN engine behind the C ABI of
+// include/frnn_mi355x.h.
+//
+// Replaces python_interface/frnn_engine.{h,cu}: workspace ownership
+// (frnn_engine.cu:23-55), auto-dispatch (frnn_engine.cu:201-246, 64-86), the
+// grid build / search / scatter pipeline (frnn_engine.cu:64-102, 224-246) and
+// the host path search()/get_results() (frnn_engine.cu:104-193, 252-258).
+//
+// Differences by design: arguments are validated before any HIP call and a
+// status is returned instead of silently overflowing; every kernel is launched
+// on one stream (the null stream unless the caller sets one) and the call
+// synchronises that stream once at the end; the dim- and K-dependent
+// workspaces are sized on first use instead of for a fixed D <= 32
+// (frnn_engine.cu:26-28).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "frnn_internal.hpp"
+#include "frnn_mi355x.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* what) {
+    g_last_error = what;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return FRNN_ERR_HIP;
+}
+
+#define HIP_TRY(call, what)                          \
+    do {                                             \
+        hipError_t e_ = (call);                      \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+#define ST_TRY(call)                \
+    do {                            \
+        int s_ = (call);            \
+        if (s_ != FRNN_OK) return s_; \
+    } while (0)
+
+int launch_status(int rc, const char* what) {
+    if (rc == 0) return FRNN_OK;
+    if (rc == 3) return hip_fail(frnn::last_launch_error(), what);
+    return fail(rc == 2 ? FRNN_ERR_CAPACITY : FRNN_ERR_INVALID_ARGUMENT, what);
+}
+
+long long ipow_sat(long long b, int e, long long cap) {
+    long long v = 1;
+    for (int i = 0; i < e; ++i) {
+        if (v > cap / (b > 0 ? b : 1)) return cap + 1;
+        v *= b;
+    }
+    return v;
+}
+
+template <typename T>
+int grow(T** p, size_t* have, size_t need_elems, const char* what) {
+    const size_t need = need_elems * sizeof(T);
+    if (*have >= need && *p) return FRNN_OK;
+    if (*p) {
+        (void)hipFree(*p);
+        *p = nullptr;
+        *have = 0;
+    }
+    HIP_TRY(hipMalloc((void**)p, need), what);
+    *have = need;
+    return FRNN_OK;
+}
+
+}  // namespace
+
+struct frnn_engine {
+    int max_p = 0;
+    hipStream_t stream = nullptr;
+    int* cell_of = nullptr;
+    int* rank = nullptr;
+    int* sorted_idx = nullptr;
+    int* inv = nullptr;
+    int* cnt = nullptr;
+    int* start = nullptr;
+    int* partials = nullptr;
+    unsigned long long* counters = nullptr;
+    int* out_idx = nullptr;
+    float* out_dist = nullptr;
+    float* aos = nullptr;
+    size_t aos_bytes = 0;
+    unsigned long long* lists = nullptr;
+    size_t lists_bytes = 0;
+    float* h2d_points = nullptr;  // search() staging (frnn_engine.cu:27 d_points)
+    size_t h2d_bytes = 0;
+    frnn_plan_t last_plan{};
+    bool has_result = false;
+    int last_N = 0, last_K = 0;
+    bool profiling = false;
+    hipEvent_t ev[FRNN_NUM_STAGES + 1] = {};
+    float stage_ms[FRNN_NUM_STAGES] = {};
+    long long ctr[FRNN_NUM_COUNTERS] = {};
+};
+
+namespace {
+
+void release(frnn_engine* e) {
+    void* bufs[] = {e->cell_of, e->rank, e->sorted_idx, e->inv, e->cnt, e->start, e->partials,
+                    e->counters, e->out_idx, e->out_dist, e->aos, e->lists, e->h2d_points};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    for (auto& ev : e->ev)
+        if (ev) (void)hipEventDestroy(ev);
+}
+
+// The whole device pipeline of search_gpu on an SoA device input.
+int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius) {
+    frnn_plan_t plan;
+    ST_TRY(frnn_make_plan(N, dim, K, radius, &plan));
+    e->last_plan = plan;
+    e->has_result = false;
+    if (plan.path == FRNN_PATH_EMPTY) {
+        e->has_result = true;
+        e->last_N = 0;
+        e->last_K = K;
+        return FRNN_OK;
+    }
+    const int ds = frnn::aos_stride(dim);
+    const int cap = frnn::list_capacity(K);
+    ST_TRY(grow(&e->aos, &e->aos_bytes, (size_t)N * ds, "allocating AoS point rows"));
+    ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)N * cap, "allocating candidate lists"));
+
+    hipStream_t s = e->stream;
+    const bool grid = plan.path != FRNN_PATH_BRUTEFORCE;
+    if (e->profiling) {
+        ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * (FRNN_NUM_COUNTERS + 1), 0, s),
+                             "clearing counters"));
+        HIP_TRY(hipEventRecord(e->ev[0], s), "event record");
+    }
+    auto mark = [&](int i) -> int {
+        if (e->profiling) HIP_TRY(hipEventRecord(e->ev[i], s), "event record");
+        return FRNN_OK;
+    };
+    if (grid) {
+        // memset + CountPointsNDKernel + thrust scan + CountingSort (frnn_engine.cu:89-96, 159-174)
+        ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, plan.cells + 1, 0, s), "zero-fill cells"));
+        ST_TRY(mark(1));
+        ST_TRY(launch_status(frnn::launch_bin_count(d_pts, N, plan.grid_dim, plan.res, plan.inv_cell,
+                                                    e->cell_of, e->rank, e->cnt, s),
+                             "bin/count launch"));
+        ST_TRY(mark(2));
+        ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)plan.cells + 1, e->start,
+                                                         e->partials, s),
+                             "scan launch"));
+        ST_TRY(mark(3));
+        ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start,
+                                                  e->sorted_idx, e->inv, e->aos, s),
+                             "reorder launch"));
+    } else {
+        ST_TRY(mark(1));
+        ST_TRY(mark(2));
+        ST_TRY(mark(3));
+        ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, s), "transpose launch"));
+    }
+    ST_TRY(mark(4));
+    ST_TRY(launch_status(frnn::launch_search(e->aos, grid ? e->sorted_idx : nullptr,
+                                             grid ? e->start : nullptr, N, dim, K, plan, e->lists,
+                                             cap, e->profiling ? e->counters : nullptr, s),
+                         "search launch"));
+    ST_TRY(mark(5));
+    ST_TRY(launch_status(frnn::launch_unpermute(e->lists, cap, grid ? e->inv : nullptr, N, K,
+                                                e->out_idx, e->out_dist, s),
+                         "unpermute launch"));
+    ST_TRY(mark(6));
+    HIP_TRY(hipStreamSynchronize(s), "search pipeline");
+    if (e->profiling) {
+        for (int i = 0; i < FRNN_NUM_STAGES; ++i)
+            HIP_TRY(hipEventElapsedTime(&e->stage_ms[i], e->ev[i], e->ev[i + 1]), "event timing");
+        unsigned long long c[FRNN_NUM_COUNTERS + 1];
+        HIP_TRY(hipMemcpy(c, e->counters, sizeof(c), hipMemcpyDeviceToHost), "reading counters");
+        for (int i = 0; i < FRNN_NUM_COUNTERS; ++i) e->ctr[i] = (long long)c[i];
+        if (c[FRNN_NUM_COUNTERS] != 0)
+            return fail(FRNN_ERR_HIP, "internal list/queue capacity overflow in the search kernel");
+    }
+    e->has_result = true;
+    e->last_N = N;
+    e->last_K = K;
+    return FRNN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* frnn_status_string(int status) {
+    switch (status) {
+        case FRNN_OK: return "ok";
+        case FRNN_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case FRNN_ERR_CAPACITY: return "capacity exceeded";
+        case FRNN_ERR_HIP: return "HIP runtime error";
+        case FRNN_ERR_NO_DEVICE: return "no HIP device";
+        case FRNN_ERR_STATE: return "invalid engine state";
+        default: return "unknown status";
+    }
+}
+
+const char* frnn_last_error(void) { return g_last_error.c_str(); }
+
+int frnn_version(void) { return 1; }
+
+int frnn_validate(int max_points, int N, int dim, int K, float radius) {
+    if (N < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "N must be >= 0");
+    if (max_points > 0 && N > max_points) return fail(FRNN_ERR_CAPACITY, "N exceeds max_points");
+    if (dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "dim must be in [1, 128]");
+    if (K < 1 || K > FRNN_MAX_K) return fail(FRNN_ERR_INVALID_ARGUMENT, "K must be in [1, 128]");
+    if (!(radius > 0.0f) || !std::isfinite(radius))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "radius must be finite and > 0");
+    return FRNN_OK;
+}
+
+int frnn_make_plan(int N, int dim, int K, float radius, frnn_plan_t* out) {
+    if (!out) return fail(FRNN_ERR_INVALID_ARGUMENT, "null plan pointer");
+    ST_TRY(frnn_validate(0, N, dim, K, radius));
+    frnn_plan_t p{};
+    p.r2 = radius * radius;
+    p.cell_size = radius;
+    p.inv_cell = 1.0f / radius;
+    if (N == 0) {
+        p.path = FRNN_PATH_EMPTY;
+        *out = p;
+        return FRNN_OK;
+    }
+    // frnn_engine.cu:201-213: res = ceil((max-min)/cell) in fp32, cells = res^dim in double
+    const float cr = std::ceil((1.0f - 0.0f) / radius);
+    const int res = cr >= 1073741824.0f ? 1073741824 : (int)cr;
+    const double total_d = std::pow((double)res, dim);
+    const bool feasible = total_d <= 1000000.0;
+    const long long total = feasible ? (long long)total_d : 0;
+    // frnn_engine.cu:215-219: small-problem brute-force rule
+    const long long kBF = 2000000LL;
+    const long long sel = std::max(1LL, (long long)(K + 7) / 8);
+    const long long db = ((long long)N * dim > kBF) ? (kBF + 1LL) : (long long)N * dim;
+    const bool use_bf = (db <= kBF / sel) && ((long long)N <= kBF / (db * sel));
+    const long long shell = ipow_sat(3, dim, (long long)4e18);
+    if (use_bf) {
+        p.path = FRNN_PATH_BRUTEFORCE;
+    } else if (res <= 1 || !feasible || shell >= total) {
+        // frnn_engine.cu:64-86: grid on the first g coordinates, else brute force
+        const int g = (dim > 4) ? 4 : std::min(dim, 3);
+        const int r2res = std::max(res, 2);
+        const double tc = std::pow((double)r2res, g);
+        const long long gshell = ipow_sat(3, g, (long long)4e18);
+        if (tc > 1000000.0 || gshell >= (long long)tc) {
+            p.path = FRNN_PATH_BRUTEFORCE;
+        } else {
+            p.path = FRNN_PATH_GRID_FIRST;
+            p.grid_dim = g;
+            p.res = r2res;
+            p.cells = (long long)tc;
+        }
+    } else {
+        p.path = FRNN_PATH_GRID_FULL;
+        p.grid_dim = dim;
+        p.res = res;
+        p.cells = total;
+        p.rev_order = (dim == 3) ? 1 : 0;   // find_nbrs.cu:474-477 (D=3 AoS path)
+    }
+    *out = p;
+    return FRNN_OK;
+}
+
+int frnn_aos_stride(int dim) { return (dim < 1 || dim > FRNN_MAX_DIM) ? -1 : frnn::aos_stride(dim); }
+int frnn_list_capacity(int K) { return (K < 1 || K > FRNN_MAX_K) ? -1 : frnn::list_capacity(K); }
+int frnn_scan_partials_count(int n) { return n < 0 ? -1 : frnn::scan_partials_count(n); }
+
+int frnn_engine_create(int max_points, frnn_engine_t** out) {
+    if (!out) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine pointer");
+    *out = nullptr;
+    if (max_points < 1) return fail(FRNN_ERR_INVALID_ARGUMENT, "max_points must be >= 1");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+        (void)hipGetLastError();
+        return fail(FRNN_ERR_NO_DEVICE, "no HIP device visible");
+    }
+    frnn_engine* e = new frnn_engine();
+    e->max_p = max_points;
+    const size_t P = (size_t)max_points;
+    const size_t C = (size_t)FRNN_MAX_CELLS + 1;
+    hipError_t err = hipSuccess;
+    auto alloc = [&](void** p, size_t bytes) {
+        if (err == hipSuccess) err = hipMalloc(p, bytes);
+    };
+    alloc((void**)&e->cell_of, P * sizeof(int));
+    alloc((void**)&e->rank, P * sizeof(int));
+    alloc((void**)&e->sorted_idx, P * sizeof(int));
+    alloc((void**)&e->inv, P * sizeof(int));
+    alloc((void**)&e->cnt, C * sizeof(int));
+    alloc((void**)&e->start, C * sizeof(int));
+    alloc((void**)&e->partials, (size_t)frnn::scan_partials_count((int)C) * sizeof(int));
+    alloc((void**)&e->counters, 4 * sizeof(unsigned long long));
+    // engine-owned outputs sized max_points*128 as the reference (frnn_engine.cu:39-40)
+    alloc((void**)&e->out_idx, P * FRNN_MAX_K * sizeof(int));
+    alloc((void**)&e->out_dist, P * FRNN_MAX_K * sizeof(float));
+    for (auto& ev : e->ev)
+        if (err == hipSuccess) err = hipEventCreate(&ev);
+    if (err != hipSuccess) {
+        int st = hip_fail(err, "allocating engine workspace");
+        release(e);
+        delete e;
+        return st;
+    }
+    *out = e;
+    return FRNN_OK;
+}
+
+int frnn_engine_destroy(frnn_engine_t* e) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    else (void)hipDeviceSynchronize();
+    release(e);
+    delete e;
+    return FRNN_OK;
+}
+
+int frnn_engine_max_points(const frnn_engine_t* e, int* out) {
+    if (!e || !out) return fail(FRNN_ERR_INVALID_ARGUMENT, "null pointer");
+    *out = e->max_p;
+    return FRNN_OK;
+}
+
+int frnn_engine_set_stream(frnn_engine_t* e, void* stream) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    e->stream = (hipStream_t)stream;
+    return FRNN_OK;
+}
+
+int frnn_engine_search_gpu(frnn_engine_t* e, const float* d_pts, int N, int dim, int K, float radius,
+                           int** d_idxs, float** d_dists) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    ST_TRY(frnn_validate(e->max_p, N, dim, K, radius));
+    if (!d_pts && N > 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device points");
+    ST_TRY(run_pipeline(e, d_pts, N, dim, K, radius));
+    if (d_idxs) *d_idxs = e->out_idx;
+    if (d_dists) *d_dists = e->out_dist;
+    return FRNN_OK;
+}
+
+int frnn_engine_search(frnn_engine_t* e, const float* h_pts, long long n_values, int K, float radius,
+                       int* h_idxs, float* h_dists) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    if (!h_pts || !h_idxs || !h_dists) return fail(FRNN_ERR_INVALID_ARGUMENT, "null host pointer");
+    // frnn_engine.cu:108-109: dim = size / max_points, N = max_points
+    if (n_values <= 0 || n_values % e->max_p != 0)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "len(points) must be a positive multiple of max_points");
+    const long long dimll = n_values / e->max_p;
+    if (dimll > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "dim must be in [1, 128]");
+    const int dim = (int)dimll;
+    const int N = e->max_p;
+    ST_TRY(frnn_validate(e->max_p, N, dim, K, radius));
+    // AoS -> SoA on the host, then H2D (frnn_engine.cu:113-117)
+    std::vector<float> soa((size_t)N * dim);
+    for (int i = 0; i < N; ++i)
+        for (int d = 0; d < dim; ++d) soa[(size_t)d * N + i] = h_pts[(size_t)i * dim + d];
+    ST_TRY(grow(&e->h2d_points, &e->h2d_bytes, soa.size(), "allocating staging points"));
+    HIP_TRY(hipMemcpyAsync(e->h2d_points, soa.data(), soa.size() * sizeof(float), hipMemcpyHostToDevice,
+                           e->stream),
+            "copying points to device");
+    ST_TRY(run_pipeline(e, e->h2d_points, N, dim, K, radius));
+    // D2H and SoA -> AoS (frnn_engine.cu:179-191)
+    std::vector<int> ti((size_t)N * K);
+    std::vector<float> td((size_t)N * K);
+    HIP_TRY(hipMemcpy(ti.data(), e->out_idx, ti.size() * sizeof(int), hipMemcpyDeviceToHost),
+            "copying indices to host");
+    HIP_TRY(hipMemcpy(td.data(), e->out_dist, td.size() * sizeof(float), hipMemcpyDeviceToHost),
+            "copying distances to host");
+    for (int k = 0; k < K; ++k)
+        for (int i = 0; i < N; ++i) {
+            h_idxs[(size_t)i * K + k] = ti[(size_t)k * N + i];
+            h_dists[(size_t)i * K + k] = td[(size_t)k * N + i];
+        }
+    return FRNN_OK;
+}
+
+int frnn_engine_get_results(frnn_engine_t* e, int N, int K, int* h_idxs, float* h_dists) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    if (!e->has_result) return fail(FRNN_ERR_STATE, "get_results called before search_gpu");
+    if (N < 0 || K < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "N and K must be >= 0");
+    const size_t n = (size_t)N * (size_t)K;
+    if (n > (size_t)e->max_p * FRNN_MAX_K) return fail(FRNN_ERR_CAPACITY, "N*K exceeds the output buffers");
+    if (n == 0) return FRNN_OK;
+    if (!h_idxs || !h_dists) return fail(FRNN_ERR_INVALID_ARGUMENT, "null host pointer");
+    HIP_TRY(hipMemcpy(h_idxs, e->out_idx, n * sizeof(int), hipMemcpyDeviceToHost), "copying indices");
+    HIP_TRY(hipMemcpy(h_dists, e->out_dist, n * sizeof(float), hipMemcpyDeviceToHost), "copying distances");
+    return FRNN_OK;
+}
+
+int frnn_engine_last_plan(const frnn_engine_t* e, frnn_plan_t* out) {
+    if (!e || !out) return fail(FRNN_ERR_INVALID_ARGUMENT, "null pointer");
+    *out = e->last_plan;
+    return FRNN_OK;
+}
+
+int frnn_engine_set_profiling(frnn_engine_t* e, int enable) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    e->profiling = enable != 0;
+    return FRNN_OK;
+}
+
+int frnn_engine_stage_times(const frnn_engine_t* e, float* ms, int n) {
+    if (!e || !ms) return fail(FRNN_ERR_INVALID_ARGUMENT, "null pointer");
+    for (int i = 0; i < n && i < FRNN_NUM_STAGES; ++i) ms[i] = e->stage_ms[i];
+    return FRNN_OK;
+}
+
+int frnn_engine_counters(const frnn_engine_t* e, long long* out, int n) {
+    if (!e || !out) return fail(FRNN_ERR_INVALID_ARGUMENT, "null pointer");
+    for (int i = 0; i < n && i < FRNN_NUM_COUNTERS; ++i) out[i] = e->ctr[i];
+    return FRNN_OK;
+}
+
+// ---- kernel launch seam ----------------------------------------------------
+
+int frnn_launch_bin_count(const float* d_pts, int N, int grid_dim, int res, float inv_cell,
+                          long long cells, int* d_cell_of, int* d_rank, int* d_cnt, void* stream) {
+    if (N < 0 || grid_dim < 1 || grid_dim > 9 || res < 1 || cells < 1 || cells > FRNN_MAX_CELLS)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "bad bin/count geometry");
+    if (ipow_sat(res, grid_dim, (long long)4e18) != cells)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "cells must equal res^grid_dim");
+    if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_cnt))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    hipStream_t s = (hipStream_t)stream;
+    ST_TRY(launch_status(frnn::launch_fill_i32(d_cnt, cells + 1, 0, s), "zero-fill cells"));
+    return launch_status(frnn::launch_bin_count(d_pts, N, grid_dim, res, inv_cell, d_cell_of, d_rank,
+                                                d_cnt, s),
+                         "bin/count launch");
+}
+
+int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partials, void* stream) {
+    if (n < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "n must be >= 0");
+    if (n > 0 && (!d_in || !d_out || !d_partials)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    return launch_status(frnn::launch_exclusive_scan(d_in, n, d_out, d_partials, (hipStream_t)stream),
+                         "scan launch");
+}
+
+int frnn_launch_reorder(const float* d_pts, int N, int dim, const int* d_cell_of, const int* d_rank,
+                        const int* d_start, int* d_sorted_idx, int* d_inv, float* d_sorted_aos,
+                        void* stream) {
+    if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
+    if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_start || !d_sorted_idx || !d_inv || !d_sorted_aos))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_sorted_idx,
+                                              d_inv, d_sorted_aos, (hipStream_t)stream),
+                         "reorder launch");
+}
+
+int frnn_launch_transpose(const float* d_pts, int N, int dim, float* d_aos, void* stream) {
+    if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
+    if (N > 0 && (!d_pts || !d_aos)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    return launch_status(frnn::launch_transpose(d_pts, N, dim, d_aos, (hipStream_t)stream),
+                         "transpose launch");
+}
+
+int frnn_launch_find_nbrs(const float* d_aos, const int* d_sorted_idx, const int* d_start, int N, int dim,
+                          int K, const frnn_plan_t* plan, unsigned long long* d_lists, int list_cap,
+                          unsigned long long* d_counters, void* stream) {
+    if (!plan) return fail(FRNN_ERR_INVALID_ARGUMENT, "null plan");
+    ST_TRY(frnn_validate(0, N, dim, K, plan->cell_size));
+    if (plan->path == FRNN_PATH_EMPTY || N == 0) return FRNN_OK;
+    if (list_cap < frnn::list_capacity(K)) return fail(FRNN_ERR_INVALID_ARGUMENT, "list_cap too small");
+    const bool grid = plan->path != FRNN_PATH_BRUTEFORCE;
+    if (!d_aos || !d_lists || (grid && (!d_sorted_idx || !d_start)))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (grid && (plan->grid_dim < 1 || plan->grid_dim > 9 || plan->grid_dim > dim || plan->res < 1 ||
+                 ipow_sat(plan->res, plan->grid_dim, (long long)4e18) != plan->cells ||
+                 plan->cells > FRNN_MAX_CELLS))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "inconsistent grid plan");
+    if (plan->rev_order && (!grid || dim != 3)) return fail(FRNN_ERR_INVALID_ARGUMENT, "reversed order is D=3 grid only");
+    return launch_status(frnn::launch_search(d_aos, d_sorted_idx, d_start, N, dim, K, *plan, d_lists,
+                                             list_cap, d_counters, (hipStream_t)stream),
+                         "search launch");
+}
+
+int frnn_launch_unpermute(const unsigned long long* d_lists, int list_cap, const int* d_inv, int N, int K,
+                          int* d_idxs, float* d_dists, void* stream) {
+    if (N < 0 || K < 1 || K > FRNN_MAX_K || list_cap < K)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N, K or list_cap");
+    if (N > 0 && (!d_lists || !d_idxs || !d_dists)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    return launch_status(frnn::launch_unpermute(d_lists, list_cap, d_inv, N, K, d_idxs, d_dists,
+                                                (hipStream_t)stream),
+                         "unpermute launch");
+}
+
+}  // extern "C"

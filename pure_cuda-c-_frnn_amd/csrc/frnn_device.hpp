@@ -1,0 +1,51 @@
+// frnn_device.hpp -- device-side helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frnn {
+
+constexpr int kWave = 64;
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// Cell coordinate of one gridded axis: floor(x * inv_cell) clamped to
+// [0, res-1] (insert_points.cu:72 with min_val = 0; the clamp replaces the
+// reference's drop of out-of-domain points, insert_points.cu:74-87).  The
+// query side of the reference truncates and clamps (find_nbrs.cu:154-155,
+// 278-279); after the clamp both agree.  NaN bins to 0 (fmaxf drops NaN).
+__device__ __forceinline__ int bin_coord(float x, float inv_cell, int res) {
+    float t = x * inv_cell;
+    float f = floorf(t);
+    f = fmaxf(f, 0.0f);
+    f = fminf(f, (float)(res - 1));
+    return (int)f;
+}
+
+// Total order on (d2, idx): non-negative fp32 bit patterns order like the
+// values, so one 64-bit compare ranks (d2, idx) lexicographically.
+__device__ __forceinline__ unsigned long long make_key(float d2, int idx) {
+    return ((unsigned long long)__float_as_uint(d2) << 32) | (unsigned int)idx;
+}
+__device__ __forceinline__ float key_d2(unsigned long long key) {
+    return __uint_as_float((unsigned int)(key >> 32));
+}
+
+__device__ __forceinline__ int wave_min_i32(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ int wave_max_i32(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ long long wave_sum_i64(long long v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+}  // namespace frnn

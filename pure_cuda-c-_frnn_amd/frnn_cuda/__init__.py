@@ -1,0 +1,240 @@
+"""frnn_cuda -- drop-in Python module for the reference FRNN engine, backed by
+the MI355X (gfx950) library libfrnn_mi355x.so through its C ABI
+(include/frnn_mi355x.h).
+
+Same module name, class, methods, argument names and result shapes as the
+reference's nanobind binding (python_interface/nanobind_module.cu:8-21):
+
+    engine = frnn_cuda.FRNNEngine(max_points=N)
+    idxs, dists = engine.search(points, K, radius)           # host AoS in/out (lists)
+    d_idx, d_dist = engine.search_gpu(dev_ptr, N, dim, K, radius)  # SoA device ptrs
+    idxs, dists = engine.get_results(N, K)                   # SoA lists of the last search_gpu
+
+Errors the reference never reported (its launch wrappers return void) raise
+ValueError for bad arguments and RuntimeError for device failures.  There is
+no CPU fallback: without the built library or a visible GPU the calls raise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+__all__ = ["FRNNEngine", "plan", "FRNNError", "LIB_PATH", "MAX_K", "MAX_DIM", "MAX_CELLS"]
+
+MAX_K = 128
+MAX_DIM = 128
+MAX_CELLS = 1_000_000
+NUM_STAGES = 6
+NUM_COUNTERS = 3
+STAGE_NAMES = ("zero_fill", "bin_count", "scan", "reorder", "search", "unpermute")
+PATH_NAMES = {-1: "empty", 0: "bruteforce", 1: "grid_full", 2: "grid_first"}
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "libfrnn_mi355x.so")
+
+_OK, _INVALID, _CAPACITY, _HIP, _NODEV, _STATE = range(6)
+
+
+class FRNNError(RuntimeError):
+    """A device-side failure reported by the engine."""
+
+
+class _Plan(ctypes.Structure):
+    _fields_ = [("path", ctypes.c_int), ("grid_dim", ctypes.c_int), ("res", ctypes.c_int),
+                ("rev_order", ctypes.c_int), ("cells", ctypes.c_longlong), ("r2", ctypes.c_float),
+                ("cell_size", ctypes.c_float), ("inv_cell", ctypes.c_float)]
+
+    def as_dict(self):
+        return {"path": PATH_NAMES.get(self.path, str(self.path)), "grid_dim": self.grid_dim,
+                "res": self.res, "rev_order": self.rev_order, "cells": self.cells,
+                "r2": self.r2, "cell_size": self.cell_size, "inv_cell": self.inv_cell}
+
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() or "
+                          f"make -C {_PKG_DIR}")
+    L = ctypes.CDLL(LIB_PATH)
+    i32, f32, i64, vp = ctypes.c_int, ctypes.c_float, ctypes.c_longlong, ctypes.c_void_p
+    pi32 = ctypes.POINTER(ctypes.c_int)
+    sig = {
+        "frnn_status_string": ([i32], ctypes.c_char_p),
+        "frnn_last_error": ([], ctypes.c_char_p),
+        "frnn_version": ([], i32),
+        "frnn_validate": ([i32, i32, i32, i32, f32], i32),
+        "frnn_make_plan": ([i32, i32, i32, f32, ctypes.POINTER(_Plan)], i32),
+        "frnn_aos_stride": ([i32], i32),
+        "frnn_list_capacity": ([i32], i32),
+        "frnn_scan_partials_count": ([i32], i32),
+        "frnn_engine_create": ([i32, ctypes.POINTER(vp)], i32),
+        "frnn_engine_destroy": ([vp], i32),
+        "frnn_engine_max_points": ([vp, pi32], i32),
+        "frnn_engine_search_gpu": ([vp, vp, i32, i32, i32, f32, ctypes.POINTER(vp),
+                                    ctypes.POINTER(vp)], i32),
+        "frnn_engine_search": ([vp, vp, i64, i32, f32, vp, vp], i32),
+        "frnn_engine_get_results": ([vp, i32, i32, vp, vp], i32),
+        "frnn_engine_set_stream": ([vp, vp], i32),
+        "frnn_engine_last_plan": ([vp, ctypes.POINTER(_Plan)], i32),
+        "frnn_engine_set_profiling": ([vp, i32], i32),
+        "frnn_engine_stage_times": ([vp, vp, i32], i32),
+        "frnn_engine_counters": ([vp, vp, i32], i32),
+        "frnn_launch_bin_count": ([vp, i32, i32, i32, f32, i64, vp, vp, vp, vp], i32),
+        "frnn_launch_exclusive_scan": ([vp, i32, vp, vp, vp], i32),
+        "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, vp, vp], i32),
+        "frnn_launch_transpose": ([vp, i32, i32, vp, vp], i32),
+        "frnn_launch_find_nbrs": ([vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan), vp, i32,
+                                   vp, vp], i32),
+        "frnn_launch_unpermute": ([vp, i32, vp, i32, i32, vp, vp, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _check(status, what=""):
+    if status == _OK:
+        return
+    L = _load()
+    msg = L.frnn_last_error().decode() or L.frnn_status_string(status).decode()
+    text = f"{what}: {msg}" if what else msg
+    if status in (_INVALID, _CAPACITY):
+        raise ValueError(text)
+    raise FRNNError(text)
+
+
+def plan(N, dim, K, radius):
+    """The reference's auto-dispatch decision for (N, dim, K, radius) as a dict."""
+    p = _Plan()
+    _check(_load().frnn_make_plan(int(N), int(dim), int(K), float(radius), ctypes.byref(p)), "plan")
+    return p.as_dict()
+
+
+def aos_stride(dim):
+    return _load().frnn_aos_stride(int(dim))
+
+
+def list_capacity(K):
+    return _load().frnn_list_capacity(int(K))
+
+
+def scan_partials_count(n):
+    return _load().frnn_scan_partials_count(int(n))
+
+
+class FRNNEngine:
+    """N-dimensional fixed-radius K-nearest search engine (reference: frnn_engine.h:9-55)."""
+
+    def __init__(self, max_points):
+        L = _load()
+        h = ctypes.c_void_p()
+        _check(L.frnn_engine_create(int(max_points), ctypes.byref(h)), "FRNNEngine")
+        self._h = h
+        self.max_points = int(max_points)
+
+    # -- reference API ----------------------------------------------------------
+    def search(self, points, K, radius):
+        """Host path: flat AoS points (len = max_points * dim) -> (idxs, dists) flat
+        AoS lists [i*K + k] (frnn_engine.cu:104-193)."""
+        idx, dist = self.search_numpy(points, K, radius)
+        return idx.reshape(-1).tolist(), dist.reshape(-1).tolist()
+
+    def search_gpu(self, dev_ptr, N, dim, K, radius):
+        """Device path: SoA fp32 device pointer p[d*N + i] -> (d_idxs_ptr, d_dists_ptr),
+        engine-owned SoA [k*N + i] buffers valid until the next call (frnn_engine.cu:195-250)."""
+        di, dd = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(_load().frnn_engine_search_gpu(self._handle(), ctypes.c_void_p(int(dev_ptr)),
+                                              int(N), int(dim), int(K), float(radius),
+                                              ctypes.byref(di), ctypes.byref(dd)), "search_gpu")
+        return int(di.value or 0), int(dd.value or 0)
+
+    def get_results(self, N, K):
+        """D2H copy of the last search_gpu output, SoA order [k*N + i], as lists
+        (frnn_engine.cu:252-258)."""
+        idx, dist = self.get_results_numpy(N, K)
+        return idx.tolist(), dist.tolist()
+
+    # -- numpy conveniences (same semantics, no list conversion) -----------------
+    def search_numpy(self, points, K, radius):
+        """Host path returning ([max_points, K] int32, [max_points, K] float32)."""
+        pts = np.ascontiguousarray(np.asarray(points, dtype=np.float32).reshape(-1))
+        n = pts.size
+        if n == 0 or n % self.max_points:
+            raise ValueError("len(points) must be a positive multiple of max_points")
+        K = int(K)
+        if not 1 <= K <= MAX_K:
+            raise ValueError("K must be in [1, 128]")
+        idx = np.empty((self.max_points, K), dtype=np.int32)
+        dist = np.empty((self.max_points, K), dtype=np.float32)
+        _check(_load().frnn_engine_search(self._handle(), pts.ctypes.data_as(ctypes.c_void_p),
+                                          n, K, float(radius),
+                                          idx.ctypes.data_as(ctypes.c_void_p),
+                                          dist.ctypes.data_as(ctypes.c_void_p)), "search")
+        return idx, dist
+
+    def get_results_numpy(self, N, K):
+        n = int(N) * int(K)
+        idx = np.empty(max(n, 0), dtype=np.int32)
+        dist = np.empty(max(n, 0), dtype=np.float32)
+        _check(_load().frnn_engine_get_results(self._handle(), int(N), int(K),
+                                               idx.ctypes.data_as(ctypes.c_void_p),
+                                               dist.ctypes.data_as(ctypes.c_void_p)), "get_results")
+        return idx, dist
+
+    # -- engine controls ----------------------------------------------------------
+    def set_stream(self, stream):
+        """Launch on a HIP stream (int handle, e.g. torch.cuda.current_stream().cuda_stream)."""
+        _check(_load().frnn_engine_set_stream(self._handle(), ctypes.c_void_p(int(stream or 0))),
+               "set_stream")
+
+    def last_plan(self):
+        p = _Plan()
+        _check(_load().frnn_engine_last_plan(self._handle(), ctypes.byref(p)), "last_plan")
+        return p.as_dict()
+
+    def set_profiling(self, enable=True):
+        _check(_load().frnn_engine_set_profiling(self._handle(), int(bool(enable))), "set_profiling")
+
+    def stage_times(self):
+        """Per-stage milliseconds of the last profiled search (HIP events)."""
+        ms = np.zeros(NUM_STAGES, dtype=np.float32)
+        _check(_load().frnn_engine_stage_times(self._handle(), ms.ctypes.data_as(ctypes.c_void_p),
+                                               NUM_STAGES), "stage_times")
+        return dict(zip(STAGE_NAMES, (float(x) for x in ms)))
+
+    def counters(self):
+        c = np.zeros(NUM_COUNTERS, dtype=np.int64)
+        _check(_load().frnn_engine_counters(self._handle(), c.ctypes.data_as(ctypes.c_void_p),
+                                            NUM_COUNTERS), "counters")
+        return {"shell_candidates": int(c[0]), "filter_hits": int(c[1]), "accepted": int(c[2])}
+
+    def close(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            _load().frnn_engine_destroy(h)
+        self._h = None
+
+    def _handle(self):
+        if getattr(self, "_h", None) is None or not self._h.value:
+            raise ValueError("engine is closed")
+        return self._h
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

@@ -1,0 +1,119 @@
+"""C-ABI and host-logic tests that need no GPU."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import frnn_cuda
+import frnn_oracle as O
+from conftest import ROOT, gpu_visible
+from test_oracle_pins import DISPATCH_TABLE
+
+HEADER = os.path.join(ROOT, "include", "frnn_mi355x.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(frnn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(frnn_cuda.LIB_PATH)
+    names = declared_functions()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_declared_symbols():
+    L = frnn_cuda._load()
+    for n in declared_functions():
+        assert getattr(L, n).restype is not None or n == "frnn_status_string"
+
+
+@pytest.mark.parametrize("args,want", DISPATCH_TABLE)
+def test_plan_matches_dispatch_table(args, want):
+    p = frnn_cuda.plan(*args)
+    assert (p["path"], p["grid_dim"], p["res"]) == want
+
+
+def test_plan_matches_oracle_on_random_inputs():
+    rs = np.random.RandomState(21)
+    for _ in range(3000):
+        N = int(rs.choice([1, 7, 100, 577, 578, 5000, 100000, 2000000]))
+        D = int(rs.randint(1, 129))
+        K = int(rs.randint(1, 129))
+        r = float(np.float32(10.0 ** rs.uniform(-3.5, 1.2)))
+        a, b = frnn_cuda.plan(N, D, K, r), O.plan(N, D, K, r)
+        for key in ("path", "grid_dim", "res", "cells", "rev_order"):
+            assert a[key] == b[key], (N, D, K, r, key, a, b)
+        assert a["r2"] == np.float32(np.float32(r) * np.float32(r))
+
+
+@pytest.mark.parametrize("args,status", [
+    ((10, 5, 3, 4, 0.1), 0),
+    ((10, 11, 3, 4, 0.1), 2),       # N > max_points
+    ((10, -1, 3, 4, 0.1), 1),
+    ((10, 5, 0, 4, 0.1), 1),
+    ((10, 5, 129, 4, 0.1), 1),
+    ((10, 5, 3, 0, 0.1), 1),
+    ((10, 5, 3, 129, 0.1), 1),
+    ((10, 5, 3, 4, 0.0), 1),
+    ((10, 5, 3, 4, -0.1), 1),
+    ((10, 5, 3, 4, float("nan")), 1),
+    ((10, 5, 3, 4, float("inf")), 1),
+    ((0, 5, 3, 4, 0.1), 0),          # max_points <= 0 skips the N check
+])
+def test_validate_statuses(args, status):
+    assert frnn_cuda._load().frnn_validate(*args) == status
+
+
+def test_plan_errors_raise_value_error():
+    with pytest.raises(ValueError):
+        frnn_cuda.plan(10, 3, 0, 0.1)
+    with pytest.raises(ValueError):
+        frnn_cuda.plan(10, 200, 4, 0.1)
+
+
+def test_geometry_helpers():
+    assert [frnn_cuda.aos_stride(d) for d in (1, 3, 4, 5, 12, 16, 17, 33, 128)] == \
+        [4, 4, 4, 8, 12, 16, 32, 64, 128]
+    assert frnn_cuda.aos_stride(0) == -1 and frnn_cuda.aos_stride(129) == -1
+    assert frnn_cuda.list_capacity(64) == 192 and frnn_cuda.list_capacity(0) == -1
+    assert frnn_cuda.scan_partials_count(1_000_001) == 246
+
+
+def test_status_strings():
+    L = frnn_cuda._load()
+    assert L.frnn_status_string(0) == b"ok"
+    assert L.frnn_status_string(4) == b"no HIP device"
+    assert L.frnn_version() >= 1
+
+
+def test_launch_seam_rejects_bad_geometry_without_touching_the_device():
+    L = frnn_cuda._load()
+    # cells != res^g, grid_dim out of range, null pointers: all rejected on the host
+    assert L.frnn_launch_bin_count(None, 10, 2, 4, 1.0, 15, None, None, None, None) == 1
+    assert L.frnn_launch_bin_count(None, 10, 0, 4, 1.0, 1, None, None, None, None) == 1
+    assert L.frnn_launch_bin_count(None, 10, 2, 4, 1.0, 16, None, None, None, None) == 1
+    assert L.frnn_launch_exclusive_scan(None, 5, None, None, None) == 1
+    assert L.frnn_launch_unpermute(None, 10, None, 5, 20, None, None, None) == 1
+    p = frnn_cuda._Plan()
+    assert L.frnn_make_plan(100000, 12, 32, ctypes.c_float(0.0345), ctypes.byref(p)) == 0
+    p.cells = 5
+    assert L.frnn_launch_find_nbrs(None, None, None, 100000, 12, 32, ctypes.byref(p), None, 128,
+                                   None, None) == 1
+
+
+@pytest.mark.skipif(gpu_visible(), reason="checks the no-device error path")
+def test_engine_without_device_raises():
+    with pytest.raises(frnn_cuda.FRNNError, match="no HIP device"):
+        frnn_cuda.FRNNEngine(max_points=16)
+
+
+def test_engine_rejects_bad_max_points():
+    with pytest.raises(ValueError):
+        frnn_cuda.FRNNEngine(max_points=0)

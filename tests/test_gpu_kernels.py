@@ -1,0 +1,109 @@
+"""Per-kernel parity of the grid build through the C-ABI launch seam (GPU).
+
+bin/count  vs the oracle's clamped binning and numpy bincount
+scan       vs numpy cumsum (exclusive)
+reorder    permutation / cell-order / row-copy invariants
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import frnn_cuda
+import frnn_oracle as O
+import frnn_workloads as W
+from gpu_util import device_soa, log, torch, vp
+
+pytestmark = pytest.mark.gpu
+
+
+def _build(X, g, res, inv):
+    t = torch()
+    N = X.shape[0]
+    cells = res ** g
+    L = frnn_cuda._load()
+    d = device_soa(X)
+    cell_of = t.empty(N, dtype=t.int32, device="cuda:0")
+    rank = t.empty(N, dtype=t.int32, device="cuda:0")
+    cnt = t.full((cells + 1,), -7, dtype=t.int32, device="cuda:0")
+    rc = L.frnn_launch_bin_count(vp(d), N, g, res, ctypes.c_float(inv), cells, vp(cell_of), vp(rank),
+                                 vp(cnt), None)
+    assert rc == 0
+    start = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
+    part = t.empty(frnn_cuda.scan_partials_count(cells + 1), dtype=t.int32, device="cuda:0")
+    assert L.frnn_launch_exclusive_scan(vp(cnt), cells + 1, vp(start), vp(part), None) == 0
+    D = X.shape[1]
+    ds = frnn_cuda.aos_stride(D)
+    sidx = t.empty(N, dtype=t.int32, device="cuda:0")
+    inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
+    aos = t.full((N * ds,), float("nan"), dtype=t.float32, device="cuda:0")
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(sidx), vp(inv_p),
+                                 vp(aos), None) == 0
+    t.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start,
+                                                  sidx=sidx, inv=inv_p, aos=aos).items()}
+
+
+@pytest.mark.parametrize("name,N", [("C1", 200_000), ("C2", 300_000), ("metric", 200_000)])
+def test_build_pipeline_parity(name, N):
+    w = W.config(name, N=N)
+    p = O.plan(1_000_000 if name != "C1" else N, w.D, w.K, w.radius)  # full-size grid geometry
+    g, res = p["grid_dim"], p["res"]
+    inv = np.float32(1.0) / np.float32(w.radius)
+    log(f"build parity {name} N={N} g={g} res={res}")
+    out = _build(w.X, g, res, float(inv))
+    cells = res ** g
+    want_cells = O.bin_cells(w.X, g, res, inv)
+    assert np.array_equal(out["cell_of"], want_cells)
+    cnt = np.bincount(want_cells, minlength=cells + 1)
+    assert np.array_equal(out["cnt"], cnt)
+    # ranks: within each cell, a permutation of 0..count-1
+    order = np.lexsort((out["rank"], want_cells))
+    c_sorted = want_cells[order]
+    first = np.searchsorted(c_sorted, c_sorted, side="left")
+    assert np.array_equal(out["rank"][order], np.arange(N) - first)
+    start = np.concatenate([[0], np.cumsum(cnt)[:-1]])
+    assert np.array_equal(out["start"], start)
+    sidx, inv_p = out["sidx"], out["inv"]
+    assert np.array_equal(np.sort(sidx), np.arange(N))
+    assert np.array_equal(sidx[inv_p], np.arange(N))
+    assert np.all(np.diff(want_cells[sidx]) >= 0)
+    ds = frnn_cuda.aos_stride(w.D)
+    rows = out["aos"].reshape(N, ds)
+    assert np.array_equal(rows[:, :w.D], w.X[sidx])
+    assert np.all(rows[:, w.D:] == 0)
+
+
+@pytest.mark.parametrize("n", [1, 2, 4095, 4096, 4097, 100_003, 1_000_001, 4096 * 4096])
+def test_exclusive_scan(n):
+    t = torch()
+    rs = np.random.RandomState(n % 1000)
+    a = rs.randint(0, 64, n).astype(np.int32)
+    if n > 1:
+        a[-1] = 0
+    d_in = t.from_numpy(a).to("cuda:0")
+    d_out = t.full((n,), -1, dtype=t.int32, device="cuda:0")
+    part = t.empty(frnn_cuda.scan_partials_count(n), dtype=t.int32, device="cuda:0")
+    log(f"scan n={n}")
+    assert frnn_cuda._load().frnn_launch_exclusive_scan(vp(d_in), n, vp(d_out), vp(part), None) == 0
+    t.cuda.synchronize()
+    want = np.concatenate([[0], np.cumsum(a.astype(np.int64))[:-1]])
+    assert np.array_equal(d_out.cpu().numpy().astype(np.int64), want)
+
+
+def test_scan_rejects_oversize():
+    t = torch()
+    assert frnn_cuda._load().frnn_launch_exclusive_scan(None, 4096 * 4096 + 1, None, None, None) == 1
+    n = 4096 * 4096 + 1
+    d = t.zeros(n, dtype=t.int32, device="cuda:0")
+    part = t.empty(frnn_cuda.scan_partials_count(n), dtype=t.int32, device="cuda:0")
+    assert frnn_cuda._load().frnn_launch_exclusive_scan(vp(d), n, vp(d), vp(part), None) == 2
+
+
+def test_bin_count_out_of_domain_and_nan():
+    X = np.array([[-5.0, 0.5], [0.5, 7.0], [1.0, 1.0], [np.nan, 0.2], [0.0, -0.0], [0.9999, 0.25]],
+                 np.float32)
+    res, inv = 4, float(np.float32(1.0) / np.float32(0.25))
+    out = _build(X, 2, res, inv)
+    assert np.array_equal(out["cell_of"], O.bin_cells(X, 2, res, np.float32(inv)))
+    assert list(out["cell_of"][:3]) == [0 + 4 * 2, 2 + 4 * 3, 3 + 4 * 3]

@@ -1,0 +1,206 @@
+"""End-to-end parity of the HIP engine with the CPU oracle (GPU).
+
+Bar: bit-exact neighbour indices, counts and distances on every compared row
+(rows are the K smallest (d2, idx) keys in ascending order, padded (r2, -1)).
+Full-size BASELINE configs are checked on sampled queries against the oracle
+run over the full database, plus size-independent row properties.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import frnn_cuda
+import frnn_oracle as O
+import frnn_workloads as W
+from conftest import ROOT
+from gpu_util import assert_rows_equal, device_soa, engine_search, log, torch
+from test_oracle_pins import CASES, unit_cloud
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("label,D,k,N,r,K,path", CASES)
+def test_paths_match_oracle(label, D, k, N, r, K, path):
+    X = unit_cloud(N, D, k, 11)
+    X[7] = X[3]
+    log(f"case {label}: N={N} D={D} K={K} r={r}")
+    gi, gd, plan = engine_search(X, K, r)
+    assert plan["path"] == path
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, label)
+
+
+EDGE = [
+    # label, D, k, N, radius, K
+    ("n1", 3, 3, 1, 0.1, 4),
+    ("n31", 16, 4, 31, 0.4, 8),
+    ("n33_k1", 12, 3, 33, 0.5, 1),
+    ("k128_grid", 16, 4, 3000, 0.2, 128),
+    ("k128_bf", 32, 4, 2000, 0.6, 128),
+    ("k_gt_n", 3, 3, 40, 0.5, 64),
+    ("d20_pad", 20, 4, 2500, 0.6, 16),
+    ("d64", 64, 4, 2000, 0.6, 32),
+    ("d128", 128, 4, 1500, 0.8, 128),
+    ("d9_full", 9, 9, 4000, 0.25, 16),
+]
+
+
+@pytest.mark.parametrize("label,D,k,N,r,K", EDGE)
+def test_edge_shapes(label, D, k, N, r, K):
+    X = unit_cloud(N, D, k, 5)
+    log(f"edge {label}: N={N} D={D} K={K} r={r} plan={O.plan(N, D, K, r)['path']}")
+    gi, gd, _ = engine_search(X, K, r)
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, label)
+
+
+def test_duplicates_and_ties():
+    rs = np.random.RandomState(3)
+    base = rs.rand(300, 3).astype(np.float32)
+    X = np.concatenate([base] * 6 + [base[:50] + np.float32(0.01)])   # many exact ties in d2
+    log("ties: N=%d" % len(X))
+    for K in (4, 16, 32):
+        gi, gd, _ = engine_search(X, K, 0.05)
+        ri, rd = O.search(X, K, 0.05)
+        assert_rows_equal(gi, gd, ri, rd, f"ties K={K}")
+
+
+def test_out_of_domain_points_are_clamped_not_dropped():
+    rs = np.random.RandomState(4)
+    X = rs.uniform(-0.3, 1.3, (5000, 3)).astype(np.float32)
+    X[:20] = 1.0                     # closed upper cell (x == 1.0 at r = 0.01 -> cell res)
+    X[20:40] = -0.0
+    for r, K in ((0.05, 16), (0.01, 8)):
+        log(f"out-of-domain r={r}")
+        gi, gd, plan = engine_search(X, K, r)
+        assert plan["path"] == "grid_full"
+        ri, rd = O.search(X, K, r)
+        assert_rows_equal(gi, gd, ri, rd, f"ood r={r}")
+        bi, bd = O.search(X, K, r, force_path=0)
+        same = np.all(np.sort(ri, 1) == np.sort(bi, 1), axis=1)
+        assert same.mean() > 0.999   # grid shell == brute force except fp-order ties at r
+
+
+def test_nan_points_have_no_neighbours():
+    rs = np.random.RandomState(6)
+    X = rs.rand(2000, 16).astype(np.float32)
+    X[5, 3] = np.nan
+    X[9, :] = np.nan
+    gi, gd, _ = engine_search(X, 8, 0.6)
+    ri, rd = O.search(X, 8, 0.6)
+    assert_rows_equal(gi, gd, ri, rd, "nan")
+    assert np.all(gi[5] == -1) and not np.any(gi == 5)
+
+
+def test_huge_radius_everything_in_range():
+    rs = np.random.RandomState(8)
+    X = rs.rand(700, 5).astype(np.float32)
+    gi, gd, _ = engine_search(X, 16, 50.0)
+    ri, rd = O.search(X, 16, 50.0)
+    assert_rows_equal(gi, gd, ri, rd, "huge r")
+    assert np.all(gi >= 0)
+
+
+def test_large_coordinates_overflow_filter():
+    # |x|^2 overflows fp32 in the MFMA filter; such pairs must still be re-evaluated exactly
+    rs = np.random.RandomState(9)
+    X = (rs.rand(600, 4) * 1e4).astype(np.float32)
+    X[:100] = (1e19 + rs.rand(100, 4) * 1e13).astype(np.float32)
+    gi, gd, _ = engine_search(X, 8, 3e13)
+    ri, rd = O.search(X, 8, 3e13)
+    assert_rows_equal(gi, gd, ri, rd, "large coords")
+
+
+def test_engine_reuse_and_api():
+    """One engine, several calls with different N/D/K (buffers grow and are reused);
+    search() host path, get_results() SoA order and search_gpu pointers."""
+    eng = frnn_cuda.FRNNEngine(max_points=6000)
+    for (N, D, k, r, K) in ((6000, 16, 4, 0.2, 32), (1000, 3, 3, 0.1, 8), (5000, 12, 3, 0.1, 64),
+                            (6000, 3, 3, 0.05, 16)):
+        X = unit_cloud(N, D, k, N)
+        gi, gd, _ = engine_search(X, K, r, engine=eng)
+        ri, rd = O.search(X, K, r)
+        assert_rows_equal(gi, gd, ri, rd, f"reuse N={N} D={D}")
+    X = unit_cloud(6000, 3, 3, 1)
+    idx_l, dist_l = eng.search(X.reshape(-1).tolist(), 16, 0.05)          # host AoS path
+    ri, rd = O.search(X, 16, 0.05)
+    assert idx_l == ri.reshape(-1).tolist()
+    assert np.array_equal(np.asarray(dist_l, np.float32), rd.reshape(-1))
+    t = torch()
+    d = device_soa(X)
+    pi, pd = eng.search_gpu(d.data_ptr(), 6000, 3, 16, 0.05)
+    assert pi and pd
+    gi_l, gd_l = eng.get_results(6000, 16)                                 # SoA lists
+    assert gi_l == ri.T.reshape(-1).tolist()
+    with pytest.raises(ValueError):
+        eng.search_gpu(d.data_ptr(), 7000, 3, 16, 0.05)                    # N > max_points
+    with pytest.raises(ValueError):
+        eng.search_gpu(d.data_ptr(), 6000, 3, 0, 0.05)
+    with pytest.raises(ValueError):
+        eng.search([0.0] * 7, 4, 0.1)
+    eng.close()
+    t.cuda.synchronize()
+
+
+def test_profiling_counters_and_stage_times():
+    X = unit_cloud(20000, 16, 4, 2)
+    eng = frnn_cuda.FRNNEngine(max_points=20000)
+    eng.set_profiling(True)
+    d = device_soa(X)
+    eng.search_gpu(d.data_ptr(), 20000, 16, 32, 0.15)
+    st = eng.stage_times()
+    c = eng.counters()
+    assert st["search"] > 0 and all(v >= 0 for v in st.values())
+    assert c["shell_candidates"] == O.shell_candidates(X, 32, 0.15)
+    assert c["filter_hits"] >= c["accepted"] > 0
+    eng.close()
+
+
+def _golden_files():
+    return sorted(glob.glob(os.path.join(ROOT, "tests", "golden", "*.npz")))
+
+
+@pytest.mark.parametrize("path", _golden_files(), ids=lambda p: os.path.basename(p))
+def test_golden_fixtures(path):
+    z = np.load(path)
+    X, K, r = z["X"], int(z["K"]), float(z["radius"])
+    log(f"golden {os.path.basename(path)}")
+    gi, gd, plan = engine_search(X, K, r)
+    assert plan["path"] == str(z["path"])
+    assert_rows_equal(gi, gd, z["idx"], z["dist"], os.path.basename(path))
+
+
+def _sample_queries(N, n, seed=1234):
+    rs = np.random.RandomState(seed)
+    return np.sort(rs.choice(N, size=min(n, N), replace=False)).astype(np.int32)
+
+
+def _row_properties(gi, gd, r2, N):
+    valid = gi >= 0
+    assert np.all(gi < N)
+    assert np.all(gd[valid] < r2)
+    assert np.all(gd[~valid] == r2)
+    # valid entries first, ascending (d2, idx)
+    assert np.all(valid[:, :-1] | ~valid[:, 1:])
+    d0, d1 = gd[:, :-1], gd[:, 1:]
+    i0, i1 = gi[:, :-1], gi[:, 1:]
+    both = valid[:, :-1] & valid[:, 1:]
+    assert np.all(~both | (d0 < d1) | ((d0 == d1) & (i0 < i1)))
+
+
+@pytest.mark.parametrize("name,nq", [("C1", 2000), ("C2", 1000), ("C3", 400), ("metric", 400),
+                                     ("C4", 300), ("C5", 200)])
+def test_baseline_configs_full_size(name, nq):
+    w = W.config(name)
+    log(f"full-size {name}: N={w.N} D={w.D} K={w.K} r={w.radius:.6f}")
+    gi, gd, plan = engine_search(w.X, w.K, w.radius)
+    r2 = np.float32(np.float32(w.radius) * np.float32(w.radius))
+    _row_properties(gi, gd, r2, w.N)
+    # every point finds itself (d2 = 0 < r2)
+    assert np.all(gd[:, 0] == 0)
+    q = _sample_queries(w.N, nq)
+    ri, rd = O.search(w.X, w.K, w.radius, query_ids=q)
+    assert_rows_equal(gi[q], gd[q], ri, rd, f"{name} sampled")
+    log(f"  path={plan['path']} mean neighbours={(gi >= 0).sum(1).mean():.1f}")
