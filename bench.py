@@ -38,15 +38,21 @@ def eprint(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_bytes(N, D, ds, g, C):
+def build_bytes(N, D, ds, g, C, refine):
     """Algorithmic HBM bytes of each build kernel (4-byte ints and floats); ds is
-    the padded AoS row length the reorder writes."""
-    return {
+    the padded row length of the AoS and filter rows the reorder writes."""
+    b = {
         "zero_fill": 4 * (C + 1),
         "bin_count": 4 * g * N + 8 * N + 8 * (C + 1),
+        "stats": 4 * D * N,
         "scan": 8 * (C + 1),
-        "reorder": 20 * N + 4 * D * N + 4 * ds * N,
+        "reorder": 20 * N + 4 * D * N + 8 * ds * N + 4 * N,
     }
+    if refine:
+        # big-cell flags scan + sub-bin count (cell, count, 2 axis coords, rank) + sub-bin scan
+        nsub = (N // 256) * 1024 + 1
+        b["refine"] = 8 * (C + 1) + 20 * N + 12 * nsub
+    return b
 
 
 def traffic_from_profiles(config):
@@ -154,7 +160,11 @@ def main():
                 "mean_kernel_ms": round(stages["search"], 4),
                 "traffic_source": traffic_src}
 
-    bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"], plan["cells"]) if plan["path"] != "bruteforce" else {}
+    if plan["path"] != "bruteforce":
+        bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"], plan["cells"],
+                         frnn_cuda.refine_workspace_bytes(w.N, w.D, w.K, w.radius) > 0)
+    else:
+        bb = {"stats": 4 * w.D * w.N, "reorder": 4 * w.D * w.N + 8 * frnn_cuda.aos_stride(w.D) * w.N + 4 * w.N}
     build = {}
     tot_b, tot_ms = 0, 0.0
     for k, b in bb.items():

@@ -60,6 +60,24 @@ typedef struct frnn_plan {
 
 typedef struct frnn_engine frnn_engine_t;
 
+/* Per-coordinate input statistics; a statistics workspace starts with
+ * FRNN_MAX_DIM of them.  mean is the centre of the MFMA filter rows (0 if not
+ * finite), var/lo/hi choose and scale the refinement axes. */
+typedef struct frnn_dim_stat {
+    float mean, var, lo, hi;
+} frnn_dim_stat_t;
+
+/* Within-cell refinement descriptor; a refinement workspace starts with it.
+ * Sub-bin of coordinate x on axis k: clamp(floor((x - lo_k) * inv_k), 0, bins_k - 1). */
+typedef struct frnn_refine_info {
+    int axes;          /* number of refinement axes (1 or 2) */
+    int bins0, bins1;  /* sub-bins per axis; bins0 * bins1 == 1024 */
+    int axis0, axis1;  /* coordinates used (highest variance first) */
+    float lo0, lo1;
+    float inv0, inv1;
+    int reserved[7];
+} frnn_refine_info_t;
+
 /* ---- host-only helpers (no HIP call) ------------------------------------ */
 
 const char* frnn_status_string(int status);
@@ -113,16 +131,18 @@ int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
 
 /* Per-stage HIP event timing (replaces the reference's FRNN_REPORT_OCCUPANCY
  * diagnostics, find_nbrs.cu:355-382).  Stages: 0 zero-fill, 1 bin+count,
- * 2 scan, 3 reorder/transpose, 4 neighbour search, 5 unpermute. */
-#define FRNN_NUM_STAGES 6
+ * 2 point statistics, 3 scan, 4 within-cell refinement, 5 reorder/transpose,
+ * 6 neighbour search, 7 unpermute. */
+#define FRNN_NUM_STAGES 8
 int frnn_engine_set_profiling(frnn_engine_t* engine, int enable);
 int frnn_engine_stage_times(const frnn_engine_t* engine, float* ms, int n);
 /* Work counters of the last profiled search: [0] shell candidates (sum over
  * queries of the points in their 3^g cells, or N per query for brute force),
- * [1] pairs passing the MFMA filter, [2] pairs accepted after the exact check.
- * A profiled search also fails with FRNN_ERR_HIP if the kernel's internal
- * capacity guards ever fired. */
-#define FRNN_NUM_COUNTERS 3
+ * [1] pairs passing the MFMA filter, [2] pairs accepted after the exact check,
+ * [3] query-candidate pairs streamed through the MFMA filter (after the
+ * window and AABB pruning).  A profiled search also fails with FRNN_ERR_HIP
+ * if the kernel's internal capacity guards ever fired. */
+#define FRNN_NUM_COUNTERS 4
 int frnn_engine_counters(const frnn_engine_t* engine, long long* out, int n);
 
 /* ---- kernel launch seam (replaces run_*, frnn_engine.cu:9-20) ------------ */
@@ -141,25 +161,55 @@ int frnn_launch_bin_count(const float* d_points_soa, int N, int grid_dim, int re
 int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partials,
                                void* stream);
 
-/* run_counting_sort / run_counting_sort_aos3 (insert_points.cu:142-164,205-226):
- * pos = d_start[cell] + rank; d_sorted_idx[pos] = i; d_inv[i] = pos; AoS row
- * pos of d_sorted_aos (stride frnn_aos_stride(dim), zero padded) = point i. */
-int frnn_launch_reorder(const float* d_points_soa, int N, int dim, const int* d_cell_of,
-                        const int* d_rank, const int* d_start, int* d_sorted_idx, int* d_inv,
-                        float* d_sorted_aos, void* stream);
+/* Per-coordinate statistics of the input (no reference counterpart): mean,
+ * variance, minimum and maximum of every coordinate, accumulated in fp64 in a
+ * fixed order.  Needs frnn_stats_workspace_bytes(dim) bytes at d_stats_ws. */
+long long frnn_stats_workspace_bytes(int dim);
+int frnn_launch_point_stats(const float* d_points_soa, int N, int dim, void* d_stats_ws, void* stream);
 
-/* Brute-force input staging: AoS copy of the SoA points in original order. */
-int frnn_launch_transpose(const float* d_points_soa, int N, int dim, float* d_aos, void* stream);
+/* Within-cell refinement (no reference counterpart: the reference's within-cell
+ * order is atomic arrival order, insert_points.cu:156-158, so any order is
+ * admissible).  For first-coordinate plans with dim > grid_dim, cells holding
+ * at least 256 points get 1024 sub-bins on the two highest-variance non-grid
+ * axes (from d_stats_ws); d_rank of their points is replaced by the sub-bin
+ * arrival slot.  Needs frnn_refine_workspace_bytes() bytes at d_ws (0 bytes:
+ * plan has no refinement, nothing to launch).  Run after the scan, before the
+ * reorder. */
+long long frnn_refine_workspace_bytes(int N, int dim, const frnn_plan_t* plan);
+int frnn_launch_refine(const float* d_points_soa, int N, int dim, const frnn_plan_t* plan,
+                       const int* d_cell_of, const int* d_cnt, int* d_rank, const void* d_stats_ws,
+                       void* d_ws, void* stream);
+
+/* run_counting_sort / run_counting_sort_aos3 (insert_points.cu:142-164,205-226):
+ * pos = d_start[cell] + rank (+ the sub-bin offset inside refined cells);
+ * d_sorted_idx[pos] = i; d_inv[i] = pos; AoS row pos of d_sorted_aos (stride
+ * frnn_aos_stride(dim), zero padded) = point i.  With d_stats_ws, row pos of
+ * d_frows gets fl(x - mean) and d_fnorm[pos] its squared norm (the MFMA filter
+ * operands).  d_refine_ws and d_stats_ws may be NULL. */
+int frnn_launch_reorder(const float* d_points_soa, int N, int dim, const int* d_cell_of,
+                        const int* d_rank, const int* d_start, const int* d_cnt,
+                        const void* d_refine_ws, long long cells, int* d_sorted_idx, int* d_inv,
+                        float* d_sorted_aos, const void* d_stats_ws, float* d_frows, float* d_fnorm,
+                        void* stream);
+
+/* Brute-force input staging: AoS copy of the SoA points in original order,
+ * plus the filter rows and norms as frnn_launch_reorder when d_stats_ws is given. */
+int frnn_launch_transpose(const float* d_points_soa, int N, int dim, float* d_aos,
+                          const void* d_stats_ws, float* d_frows, float* d_fnorm, void* stream);
 
 /* run_find_nbrs / run_find_nbrs_griddim / run_find_nbrs_aos3 / run_bruteforce
  * (find_nbrs.cu:525-633, no_grid_frnn.cu:273-326): neighbour search over the
- * plan's path.  Grid paths read the cell-sorted AoS points, d_sorted_idx and
- * d_start (cells+1 exclusive offsets); brute force reads the transposed AoS
- * points and ignores both.  Results: for sorted position s, entries
+ * plan's path.  The MFMA filter streams d_frows/d_fnorm (written by the reorder
+ * or transpose with statistics); exact distances use d_aos.  Grid paths read
+ * the cell-sorted AoS points, d_sorted_idx and
+ * d_start (cells+1 exclusive offsets), and the refinement tables when given;
+ * brute force reads the transposed AoS points and ignores them.  Results: for sorted position s, entries
  * d_lists[s*list_cap + k], k < K, hold ascending keys (bits(d2) << 32 | idx)
- * with padding (bits(r2) << 32 | 0xffffffff).  d_counters (3 u64, may be NULL)
- * accumulates the work counters. */
-int frnn_launch_find_nbrs(const float* d_aos, const int* d_sorted_idx, const int* d_start,
+ * with padding (bits(r2) << 32 | 0xffffffff).  d_counters (5 u64: the
+ * FRNN_NUM_COUNTERS work counters and a capacity-guard counter; may be NULL)
+ * accumulates the counters. */
+int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float* d_fnorm,
+                          const int* d_sorted_idx, const int* d_start, const void* d_refine_ws,
                           int N, int dim, int K, const frnn_plan_t* plan,
                           unsigned long long* d_lists, int list_cap,
                           unsigned long long* d_counters, void* stream);

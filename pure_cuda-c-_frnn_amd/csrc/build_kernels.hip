@@ -63,16 +63,20 @@ __device__ __forceinline__ int block_exclusive_scan_256(int v, int* s_tmp, int* 
     return incl - v;
 }
 
+// flag_min > 0: the scanned value is (in[i] >= flag_min), e.g. "cell is big".
+__device__ __forceinline__ int scan_value(const int* __restrict__ in, long long idx, int n, int flag_min) {
+    if (idx >= n) return 0;
+    const int v = in[idx];
+    return flag_min > 0 ? (v >= flag_min ? 1 : 0) : v;
+}
+
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int* __restrict__ in, int n,
-                                                                   int* __restrict__ partials) {
+                                                                   int* __restrict__ partials, int flag_min) {
     __shared__ int s_tmp[kScanThreads];
     const long long base = (long long)blockIdx.x * kScanTile + (long long)threadIdx.x * kScanItems;
     int sum = 0;
 #pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
-        long long idx = base + j;
-        sum += (idx < n) ? in[idx] : 0;
-    }
+    for (int j = 0; j < kScanItems; ++j) sum += scan_value(in, base + j, n, flag_min);
     int total;
     block_exclusive_scan_256(sum, s_tmp, &total);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
@@ -100,15 +104,14 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int* __rest
 
 __global__ __launch_bounds__(kScanThreads) void scan_final_kernel(const int* __restrict__ in, int n,
                                                                   const int* __restrict__ partials,
-                                                                  int* __restrict__ out) {
+                                                                  int* __restrict__ out, int flag_min) {
     __shared__ int s_tmp[kScanThreads];
     const long long base = (long long)blockIdx.x * kScanTile + (long long)threadIdx.x * kScanItems;
     int v[kScanItems];
     int sum = 0;
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) {
-        long long idx = base + j;
-        v[j] = (idx < n) ? in[idx] : 0;
+        v[j] = scan_value(in, base + j, n, flag_min);
         sum += v[j];
     }
     int total;
@@ -121,44 +124,187 @@ __global__ __launch_bounds__(kScanThreads) void scan_final_kernel(const int* __r
     }
 }
 
+// Row `pos` of the AoS array gets point i (zero padded to ds); when filter
+// rows are requested, row `pos` of frows gets fl(x - mean) and fnorm[pos] its
+// squared norm (sequential fma).
+__device__ __forceinline__ void write_rows(const float* __restrict__ pts, int N, int D, int ds, int i, int pos,
+                                           float* __restrict__ aos, const DimStat* __restrict__ st,
+                                           float* __restrict__ frows, float* __restrict__ fnorm) {
+    float4* row = reinterpret_cast<float4*>(aos + (size_t)pos * ds);
+    float4* frow = frows ? reinterpret_cast<float4*>(frows + (size_t)pos * ds) : nullptr;
+    float nrm = 0.0f;
+    for (int d = 0; d < ds; d += 4) {
+        float4 v;
+        v.x = (d + 0 < D) ? pts[(size_t)(d + 0) * N + i] : 0.0f;
+        v.y = (d + 1 < D) ? pts[(size_t)(d + 1) * N + i] : 0.0f;
+        v.z = (d + 2 < D) ? pts[(size_t)(d + 2) * N + i] : 0.0f;
+        v.w = (d + 3 < D) ? pts[(size_t)(d + 3) * N + i] : 0.0f;
+        row[d >> 2] = v;
+        if (frow) {
+            float4 f;
+            f.x = (d + 0 < D) ? v.x - st[d + 0].mean : 0.0f;
+            f.y = (d + 1 < D) ? v.y - st[d + 1].mean : 0.0f;
+            f.z = (d + 2 < D) ? v.z - st[d + 2].mean : 0.0f;
+            f.w = (d + 3 < D) ? v.w - st[d + 3].mean : 0.0f;
+            frow[d >> 2] = f;
+            nrm = fmaf(f.x, f.x, nrm);
+            nrm = fmaf(f.y, f.y, nrm);
+            nrm = fmaf(f.z, f.z, nrm);
+            nrm = fmaf(f.w, f.w, nrm);
+        }
+    }
+    if (frow) fnorm[pos] = nrm;
+}
+
 // One thread per point: SoA reads are coalesced per axis; the AoS row store
-// is ds/4 16-byte vector stores to one contiguous row.
+// is ds/4 16-byte vector stores to one contiguous row.  Points of big cells go
+// to their sub-bin's range of the cell (within-cell refinement order).
 __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ pts, int N, int D, int ds,
                                                       const int* __restrict__ cell_of,
                                                       const int* __restrict__ rank,
                                                       const int* __restrict__ start,
+                                                      const int* __restrict__ cnt,
+                                                      const RefineInfo* __restrict__ ref,
+                                                      const int* __restrict__ bidx,
+                                                      const int* __restrict__ substart,
                                                       int* __restrict__ sorted_idx,
                                                       int* __restrict__ inv,
-                                                      float* __restrict__ aos) {
+                                                      float* __restrict__ aos,
+                                                      const DimStat* __restrict__ st,
+                                                      float* __restrict__ frows,
+                                                      float* __restrict__ fnorm) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
-    const int pos = start[cell_of[i]] + rank[i];
+    const int c = cell_of[i];
+    int pos = start[c] + rank[i];
+    if (ref && cnt[c] >= kBigCell) {
+        const int L = ref->L;
+        const int q1 = sub_bin(pts[(size_t)ref->axis0 * N + i], ref->lo0, ref->inv0, ref->nb1);
+        const int q2 = L > 1 ? sub_bin(pts[(size_t)ref->axis1 * N + i], ref->lo1, ref->inv1, ref->nb2) : 0;
+        const size_t base = (size_t)bidx[c] * kSubBins;
+        pos += substart[base + q1 * ref->nb2 + q2] - substart[base];
+    }
     sorted_idx[pos] = i;
     inv[i] = pos;
-    float4* row = reinterpret_cast<float4*>(aos + (size_t)pos * ds);
-    for (int d = 0; d < ds; d += 4) {
-        float4 v;
-        v.x = (d + 0 < D) ? pts[(size_t)(d + 0) * N + i] : 0.0f;
-        v.y = (d + 1 < D) ? pts[(size_t)(d + 1) * N + i] : 0.0f;
-        v.z = (d + 2 < D) ? pts[(size_t)(d + 2) * N + i] : 0.0f;
-        v.w = (d + 3 < D) ? pts[(size_t)(d + 3) * N + i] : 0.0f;
-        row[d >> 2] = v;
+    write_rows(pts, N, D, ds, i, pos, aos, st, frows, fnorm);
+}
+
+// Per-axis statistics of coordinates g..D-1: partial sums (fp64) of x - x0
+// (x0 = the axis' first value, a shift that keeps the variance well
+// conditioned), minimum and maximum per block, reduced in a fixed order by
+// stats_setup_kernel.
+__global__ __launch_bounds__(256) void dim_stats_kernel(const float* __restrict__ pts, int N, int g, int D,
+                                                        double* __restrict__ part) {
+    __shared__ double s_sum[256], s_sq[256];
+    __shared__ float s_mn[256], s_mx[256];
+    const int t = threadIdx.x;
+    for (int d = g; d < D; ++d) {
+        const double pivot = pts[(size_t)d * N];
+        double sum = 0.0, sq = 0.0;
+        float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+        for (long long i = (long long)blockIdx.x * 256 + t; i < N; i += 256LL * gridDim.x) {
+            const float v = pts[(size_t)d * N + i];
+            const double dv = (double)v - pivot;
+            sum += dv;
+            sq += dv * dv;
+            mn = fminf(mn, v);
+            mx = fmaxf(mx, v);
+        }
+        s_sum[t] = sum; s_sq[t] = sq; s_mn[t] = mn; s_mx[t] = mx;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (t < o) {
+                s_sum[t] += s_sum[t + o];
+                s_sq[t] += s_sq[t + o];
+                s_mn[t] = fminf(s_mn[t], s_mn[t + o]);
+                s_mx[t] = fmaxf(s_mx[t], s_mx[t + o]);
+            }
+            __syncthreads();
+        }
+        if (t == 0) {
+            double* p = part + ((size_t)blockIdx.x * (D - g) + (d - g)) * 4;
+            p[0] = s_sum[0]; p[1] = s_sq[0]; p[2] = s_mn[0]; p[3] = s_mx[0];
+        }
+        __syncthreads();
     }
 }
 
-__global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ pts, int N, int D, int ds,
-                                                        float* __restrict__ aos) {
+// Reduces the per-block partials (fixed order) into one DimStat per axis.  A
+// non-finite mean (NaN or infinite data) centres at 0 instead.
+__global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restrict__ pts,
+                                                          const double* __restrict__ part, int nblk, int N, int D,
+                                                          DimStat* __restrict__ st) {
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        const double pivot = pts[(size_t)d * N];
+        double sum = 0.0, sq = 0.0;
+        float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+        for (int b = 0; b < nblk; ++b) {
+            const double* p = part + ((size_t)b * D + d) * 4;
+            sum += p[0]; sq += p[1];
+            mn = fminf(mn, (float)p[2]); mx = fmaxf(mx, (float)p[3]);
+        }
+        const double shifted = sum / N;
+        double var = sq / N - shifted * shifted;
+        if (!(var >= 0.0)) var = -1.0;        // NaN data: never preferred as an axis
+        float m = (float)(pivot + shifted);
+        if (!(m > -3.0e38f && m < 3.0e38f)) m = 0.0f;
+        st[d] = DimStat{m, (float)var, mn, mx};
+    }
+}
+
+// Picks the refinement axes among g..D-1 (largest variance first, lower index
+// on ties) and the sub-bin geometry.  One thread.
+__global__ void refine_setup_kernel(const DimStat* __restrict__ st, int g, int D, RefineInfo* __restrict__ info) {
+    if (threadIdx.x != 0) return;
+    const int nd = D - g;
+    int a0 = g, a1 = -1;
+    for (int d = g + 1; d < D; ++d)
+        if (st[d].var > st[a0].var) a0 = d;
+    for (int d = g; d < D; ++d)
+        if (d != a0 && (a1 < 0 || st[d].var > st[a1].var)) a1 = d;
+    RefineInfo r{};
+    r.L = nd >= 2 ? 2 : 1;
+    r.nb1 = r.L == 2 ? 32 : kSubBins;
+    r.nb2 = r.L == 2 ? 32 : 1;
+    r.axis0 = a0;
+    r.axis1 = r.L == 2 ? a1 : a0;
+    const float rng0 = st[a0].hi - st[a0].lo;
+    r.lo0 = st[a0].lo;
+    r.inv0 = (rng0 > 0.0f && rng0 < 3.0e38f) ? (float)r.nb1 / rng0 : 0.0f;
+    if (r.L == 2) {
+        const float rng1 = st[a1].hi - st[a1].lo;
+        r.lo1 = st[a1].lo;
+        r.inv1 = (rng1 > 0.0f && rng1 < 3.0e38f) ? (float)r.nb2 / rng1 : 0.0f;
+    }
+    if (!(r.lo0 > -3.0e38f && r.lo0 < 3.0e38f)) { r.lo0 = 0.0f; r.inv0 = 0.0f; }
+    if (!(r.lo1 > -3.0e38f && r.lo1 < 3.0e38f)) { r.lo1 = 0.0f; r.inv1 = 0.0f; }
+    *info = r;
+}
+
+// Sub-bin counting inside big cells; the arrival slot replaces the cell rank.
+__global__ __launch_bounds__(256) void sub_count_kernel(const float* __restrict__ pts, int N,
+                                                        const int* __restrict__ cell_of,
+                                                        const int* __restrict__ cnt,
+                                                        const int* __restrict__ bidx,
+                                                        const RefineInfo* __restrict__ ref,
+                                                        int* __restrict__ subcnt, int* __restrict__ rank) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
-    float4* row = reinterpret_cast<float4*>(aos + (size_t)i * ds);
-    for (int d = 0; d < ds; d += 4) {
-        float4 v;
-        v.x = (d + 0 < D) ? pts[(size_t)(d + 0) * N + i] : 0.0f;
-        v.y = (d + 1 < D) ? pts[(size_t)(d + 1) * N + i] : 0.0f;
-        v.z = (d + 2 < D) ? pts[(size_t)(d + 2) * N + i] : 0.0f;
-        v.w = (d + 3 < D) ? pts[(size_t)(d + 3) * N + i] : 0.0f;
-        row[d >> 2] = v;
-    }
+    const int c = cell_of[i];
+    if (cnt[c] < kBigCell) return;
+    const int q1 = sub_bin(pts[(size_t)ref->axis0 * N + i], ref->lo0, ref->inv0, ref->nb1);
+    const int q2 = ref->L > 1 ? sub_bin(pts[(size_t)ref->axis1 * N + i], ref->lo1, ref->inv1, ref->nb2) : 0;
+    rank[i] = atomicAdd(&subcnt[(size_t)bidx[c] * kSubBins + q1 * ref->nb2 + q2], 1);
+}
+
+__global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ pts, int N, int D, int ds,
+                                                        float* __restrict__ aos,
+                                                        const DimStat* __restrict__ st,
+                                                        float* __restrict__ frows,
+                                                        float* __restrict__ fnorm) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    write_rows(pts, N, D, ds, i, i, aos, st, frows, fnorm);
 }
 
 // One thread per original query: reads its K sorted keys (contiguous, 16-byte
@@ -209,28 +355,109 @@ int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, in
 
 int scan_partials_count(int n) { return (n + kScanTile - 1) / kScanTile + 1; }
 
-int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s) {
+int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s, int flag_min) {
     if (n <= 0) return 0;
     const int nb = (n + kScanTile - 1) / kScanTile;
     if (nb > kScanTile) return 2;
-    hipLaunchKernelGGL(scan_reduce_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials);
+    hipLaunchKernelGGL(scan_reduce_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, flag_min);
     hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partials, nb);
-    hipLaunchKernelGGL(scan_final_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out);
+    hipLaunchKernelGGL(scan_final_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out, flag_min);
+    return launch_result();
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+RefineLayout refine_layout(int N, int D, long long cells) {
+    RefineLayout L{};
+    L.max_big = N / kBigCell;
+    L.nsub = L.max_big * kSubBins + 1;
+    size_t off = 0;
+    L.info = off;     off = align256(off + sizeof(RefineInfo));
+    L.bidx = off;     off = align256(off + (size_t)(cells + 1) * sizeof(int));
+    L.subcnt = off;   off = align256(off + (size_t)L.nsub * sizeof(int));
+    L.substart = off; off = align256(off + (size_t)L.nsub * sizeof(int));
+    const int np = scan_partials_count(L.nsub > cells + 1 ? L.nsub : (int)(cells + 1));
+    L.scanpart = off; off = align256(off + (size_t)np * sizeof(int));
+    L.total = off;
+    (void)D;
+    return L;
+}
+
+StatsLayout stats_layout(int D) {
+    StatsLayout L{};
+    L.dims = 0;
+    L.part = align256((size_t)FRNN_MAX_DIM * sizeof(DimStat));
+    L.total = align256(L.part + (size_t)kStatBlocks * (D > 0 ? D : 1) * 4 * sizeof(double));
+    return L;
+}
+
+int launch_point_stats(const float* pts, int N, int D, void* stats_ws, hipStream_t s) {
+    if (N <= 0) return 0;
+    const StatsLayout L = stats_layout(D);
+    char* base = static_cast<char*>(stats_ws);
+    double* part = reinterpret_cast<double*>(base + L.part);
+    hipLaunchKernelGGL(dim_stats_kernel, dim3(kStatBlocks), dim3(256), 0, s, pts, N, 0, D, part);
+    hipLaunchKernelGGL(stats_setup_kernel, dim3(1), dim3(128), 0, s, pts, part, kStatBlocks, N, D,
+                       reinterpret_cast<DimStat*>(base + L.dims));
+    return launch_result();
+}
+
+int launch_refine(const float* pts, int N, int D, int g, long long cells, const int* cell_of, const int* cnt,
+                  int* rank, const void* stats_ws, void* ws, hipStream_t s) {
+    if (N <= 0 || D <= g) return 0;
+    const RefineLayout L = refine_layout(N, D, cells);
+    char* base = static_cast<char*>(ws);
+    RefineInfo* info = reinterpret_cast<RefineInfo*>(base + L.info);
+    int* bidx = reinterpret_cast<int*>(base + L.bidx);
+    int* subcnt = reinterpret_cast<int*>(base + L.subcnt);
+    int* substart = reinterpret_cast<int*>(base + L.substart);
+    int* scanpart = reinterpret_cast<int*>(base + L.scanpart);
+    const DimStat* st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
+    hipLaunchKernelGGL(refine_setup_kernel, dim3(1), dim3(64), 0, s, st, g, D, info);
+    int rc = launch_exclusive_scan(cnt, (int)cells + 1, bidx, scanpart, s, kBigCell);
+    if (rc) return rc;
+    rc = launch_fill_i32(subcnt, L.nsub, 0, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(sub_count_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, cell_of, cnt,
+                       bidx, info, subcnt, rank);
+    rc = launch_exclusive_scan(subcnt, L.nsub, substart, scanpart, s);
+    if (rc) return rc;
     return launch_result();
 }
 
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,
-                   int* sorted_idx, int* inv, float* aos, hipStream_t s) {
+                   const int* cnt, const void* refine_ws, long long cells, int* sorted_idx, int* inv,
+                   float* aos, const void* stats_ws, float* frows, float* fnorm, hipStream_t s) {
     if (N <= 0) return 0;
+    const RefineInfo* ref = nullptr;
+    const int* bidx = nullptr;
+    const int* substart = nullptr;
+    if (refine_ws) {
+        const RefineLayout L = refine_layout(N, D, cells);
+        const char* base = static_cast<const char*>(refine_ws);
+        ref = reinterpret_cast<const RefineInfo*>(base + L.info);
+        bidx = reinterpret_cast<const int*>(base + L.bidx);
+        substart = reinterpret_cast<const int*>(base + L.substart);
+    }
+    const DimStat* st = stats_ws ? reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) +
+                                                                    stats_layout(D).dims)
+                                 : nullptr;
+    if (!st) frows = nullptr;
     hipLaunchKernelGGL(reorder_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, D,
-                       aos_stride(D), cell_of, rank, start, sorted_idx, inv, aos);
+                       aos_stride(D), cell_of, rank, start, cnt, ref, bidx, substart, sorted_idx, inv, aos,
+                       st, frows, fnorm);
     return launch_result();
 }
 
-int launch_transpose(const float* pts, int N, int D, float* aos, hipStream_t s) {
+int launch_transpose(const float* pts, int N, int D, float* aos, const void* stats_ws, float* frows,
+                     float* fnorm, hipStream_t s) {
     if (N <= 0) return 0;
+    const DimStat* st = stats_ws ? reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) +
+                                                                    stats_layout(D).dims)
+                                 : nullptr;
+    if (!st) frows = nullptr;
     hipLaunchKernelGGL(transpose_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, D,
-                       aos_stride(D), aos);
+                       aos_stride(D), aos, st, frows, fnorm);
     return launch_result();
 }
 

@@ -26,6 +26,9 @@
 
 namespace {
 
+// public counters plus the kernel's internal capacity-guard counter
+constexpr int kCounterSlots = FRNN_NUM_COUNTERS + 1;
+
 thread_local std::string g_last_error;
 
 int fail(int status, const char* what) {
@@ -96,6 +99,14 @@ struct frnn_engine {
     float* out_dist = nullptr;
     float* aos = nullptr;
     size_t aos_bytes = 0;
+    void* refine_ws = nullptr;    // within-cell refinement tables
+    size_t refine_bytes = 0;
+    void* stats_ws = nullptr;     // per-coordinate statistics (filter centre, refinement axes)
+    size_t stats_bytes = 0;
+    float* frows = nullptr;       // centred filter rows, stride aos_stride(dim)
+    size_t frows_bytes = 0;
+    float* fnorm = nullptr;       // their squared norms
+    size_t fnorm_bytes = 0;
     unsigned long long* lists = nullptr;
     size_t lists_bytes = 0;
     float* h2d_points = nullptr;  // search() staging (frnn_engine.cu:27 d_points)
@@ -113,7 +124,8 @@ namespace {
 
 void release(frnn_engine* e) {
     void* bufs[] = {e->cell_of, e->rank, e->sorted_idx, e->inv, e->cnt, e->start, e->partials,
-                    e->counters, e->out_idx, e->out_dist, e->aos, e->lists, e->h2d_points};
+                    e->counters, e->out_idx, e->out_dist, e->aos, e->lists, e->h2d_points,
+                    e->refine_ws, e->stats_ws, e->frows, e->fnorm};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (auto& ev : e->ev)
@@ -135,12 +147,16 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     const int ds = frnn::aos_stride(dim);
     const int cap = frnn::list_capacity(K);
     ST_TRY(grow(&e->aos, &e->aos_bytes, (size_t)N * ds, "allocating AoS point rows"));
+    ST_TRY(grow(&e->frows, &e->frows_bytes, (size_t)N * ds, "allocating filter rows"));
+    ST_TRY(grow(&e->fnorm, &e->fnorm_bytes, (size_t)N, "allocating filter norms"));
     ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)N * cap, "allocating candidate lists"));
+    ST_TRY(grow((char**)&e->stats_ws, &e->stats_bytes, frnn::stats_layout(dim).total, "allocating statistics"));
 
     hipStream_t s = e->stream;
     const bool grid = plan.path != FRNN_PATH_BRUTEFORCE;
+    const void* refine = nullptr;
     if (e->profiling) {
-        ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * (FRNN_NUM_COUNTERS + 1), 0, s),
+        ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * kCounterSlots, 0, s),
                              "clearing counters"));
         HIP_TRY(hipEventRecord(e->ev[0], s), "event record");
     }
@@ -148,42 +164,60 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
         if (e->profiling) HIP_TRY(hipEventRecord(e->ev[i], s), "event record");
         return FRNN_OK;
     };
-    if (grid) {
-        // memset + CountPointsNDKernel + thrust scan + CountingSort (frnn_engine.cu:89-96, 159-174)
-        ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, plan.cells + 1, 0, s), "zero-fill cells"));
-        ST_TRY(mark(1));
+    // stage 0: zero-fill, 1: bin+count (frnn_engine.cu:89-90, 159-160)
+    if (grid) ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, plan.cells + 1, 0, s), "zero-fill cells"));
+    ST_TRY(mark(1));
+    if (grid)
         ST_TRY(launch_status(frnn::launch_bin_count(d_pts, N, plan.grid_dim, plan.res, plan.inv_cell,
                                                     e->cell_of, e->rank, e->cnt, s),
                              "bin/count launch"));
-        ST_TRY(mark(2));
+    ST_TRY(mark(2));
+    // stage 2: per-coordinate statistics (filter centre, refinement axes)
+    ST_TRY(launch_status(frnn::launch_point_stats(d_pts, N, dim, e->stats_ws, s), "statistics launch"));
+    ST_TRY(mark(3));
+    // stage 3: exclusive scan of the counts (thrust::exclusive_scan, frnn_engine.cu:91-94)
+    if (grid)
         ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)plan.cells + 1, e->start,
                                                          e->partials, s),
                              "scan launch"));
-        ST_TRY(mark(3));
-        ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start,
-                                                  e->sorted_idx, e->inv, e->aos, s),
-                             "reorder launch"));
-    } else {
-        ST_TRY(mark(1));
-        ST_TRY(mark(2));
-        ST_TRY(mark(3));
-        ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, s), "transpose launch"));
-    }
     ST_TRY(mark(4));
-    ST_TRY(launch_status(frnn::launch_search(e->aos, grid ? e->sorted_idx : nullptr,
-                                             grid ? e->start : nullptr, N, dim, K, plan, e->lists,
-                                             cap, e->profiling ? e->counters : nullptr, s),
-                         "search launch"));
+    // stage 4: within-cell refinement of big cells (first-coordinate grids with D > g)
+    if (grid && frnn::refine_axes(plan, dim) > 0) {
+        const frnn::RefineLayout L = frnn::refine_layout(N, dim, plan.cells);
+        ST_TRY(grow((char**)&e->refine_ws, &e->refine_bytes, L.total, "allocating refinement tables"));
+        refine = e->refine_ws;
+        ST_TRY(launch_status(frnn::launch_refine(d_pts, N, dim, plan.grid_dim, plan.cells, e->cell_of,
+                                                 e->cnt, e->rank, e->stats_ws, e->refine_ws, s),
+                             "refinement launch"));
+    }
     ST_TRY(mark(5));
+    // stage 5: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
+    // brute force, the AoS copy; both also write the filter rows
+    if (grid)
+        ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start, e->cnt,
+                                                  refine, plan.cells, e->sorted_idx, e->inv, e->aos,
+                                                  e->stats_ws, e->frows, e->fnorm, s),
+                             "reorder launch"));
+    else
+        ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, e->stats_ws, e->frows, e->fnorm, s),
+                             "transpose launch"));
+    ST_TRY(mark(6));
+    // stage 6: neighbour search
+    ST_TRY(launch_status(frnn::launch_search(e->aos, e->frows, e->fnorm, grid ? e->sorted_idx : nullptr,
+                                             grid ? e->start : nullptr, refine, N, dim, K, plan,
+                                             e->lists, cap, e->profiling ? e->counters : nullptr, s),
+                         "search launch"));
+    ST_TRY(mark(7));
+    // stage 7: results to the original query order (ScatterToOrigKernel)
     ST_TRY(launch_status(frnn::launch_unpermute(e->lists, cap, grid ? e->inv : nullptr, N, K,
                                                 e->out_idx, e->out_dist, s),
                          "unpermute launch"));
-    ST_TRY(mark(6));
+    ST_TRY(mark(8));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
     if (e->profiling) {
         for (int i = 0; i < FRNN_NUM_STAGES; ++i)
             HIP_TRY(hipEventElapsedTime(&e->stage_ms[i], e->ev[i], e->ev[i + 1]), "event timing");
-        unsigned long long c[FRNN_NUM_COUNTERS + 1];
+        unsigned long long c[kCounterSlots];
         HIP_TRY(hipMemcpy(c, e->counters, sizeof(c), hipMemcpyDeviceToHost), "reading counters");
         for (int i = 0; i < FRNN_NUM_COUNTERS; ++i) e->ctr[i] = (long long)c[i];
         if (c[FRNN_NUM_COUNTERS] != 0)
@@ -304,7 +338,7 @@ int frnn_engine_create(int max_points, frnn_engine_t** out) {
     alloc((void**)&e->cnt, C * sizeof(int));
     alloc((void**)&e->start, C * sizeof(int));
     alloc((void**)&e->partials, (size_t)frnn::scan_partials_count((int)C) * sizeof(int));
-    alloc((void**)&e->counters, 4 * sizeof(unsigned long long));
+    alloc((void**)&e->counters, kCounterSlots * sizeof(unsigned long long));
     // engine-owned outputs sized max_points*128 as the reference (frnn_engine.cu:39-40)
     alloc((void**)&e->out_idx, P * FRNN_MAX_K * sizeof(int));
     alloc((void**)&e->out_dist, P * FRNN_MAX_K * sizeof(float));
@@ -449,25 +483,64 @@ int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partia
                          "scan launch");
 }
 
+long long frnn_stats_workspace_bytes(int dim) {
+    if (dim < 1 || dim > FRNN_MAX_DIM) return -1;
+    return (long long)frnn::stats_layout(dim).total;
+}
+
+int frnn_launch_point_stats(const float* d_pts, int N, int dim, void* d_stats_ws, void* stream) {
+    if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
+    if (N > 0 && (!d_pts || !d_stats_ws)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    return launch_status(frnn::launch_point_stats(d_pts, N, dim, d_stats_ws, (hipStream_t)stream),
+                         "statistics launch");
+}
+
+long long frnn_refine_workspace_bytes(int N, int dim, const frnn_plan_t* plan) {
+    if (!plan || N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return -1;
+    if (frnn::refine_axes(*plan, dim) == 0 || N == 0) return 0;
+    return (long long)frnn::refine_layout(N, dim, plan->cells).total;
+}
+
+int frnn_launch_refine(const float* d_pts, int N, int dim, const frnn_plan_t* plan, const int* d_cell_of,
+                       const int* d_cnt, int* d_rank, const void* d_stats_ws, void* d_ws, void* stream) {
+    if (!plan || N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad refine arguments");
+    if (frnn::refine_axes(*plan, dim) == 0 || N == 0) return FRNN_OK;
+    if (plan->cells < 1 || plan->cells > FRNN_MAX_CELLS) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad cell count");
+    if (!d_pts || !d_cell_of || !d_cnt || !d_rank || !d_stats_ws || !d_ws)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    return launch_status(frnn::launch_refine(d_pts, N, dim, plan->grid_dim, plan->cells, d_cell_of, d_cnt, d_rank,
+                                             d_stats_ws, d_ws, (hipStream_t)stream),
+                         "refinement launch");
+}
+
 int frnn_launch_reorder(const float* d_pts, int N, int dim, const int* d_cell_of, const int* d_rank,
-                        const int* d_start, int* d_sorted_idx, int* d_inv, float* d_sorted_aos,
-                        void* stream) {
+                        const int* d_start, const int* d_cnt, const void* d_refine_ws, long long cells,
+                        int* d_sorted_idx, int* d_inv, float* d_sorted_aos, const void* d_stats_ws,
+                        float* d_frows, float* d_fnorm, void* stream) {
     if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
     if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_start || !d_sorted_idx || !d_inv || !d_sorted_aos))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_sorted_idx,
-                                              d_inv, d_sorted_aos, (hipStream_t)stream),
+    if (d_refine_ws && (!d_cnt || cells < 1 || cells > FRNN_MAX_CELLS))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "refinement needs counts and the cell count");
+    if (d_stats_ws && (!d_frows || !d_fnorm)) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need both outputs");
+    return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_cnt, d_refine_ws,
+                                              cells, d_sorted_idx, d_inv, d_sorted_aos, d_stats_ws, d_frows,
+                                              d_fnorm, (hipStream_t)stream),
                          "reorder launch");
 }
 
-int frnn_launch_transpose(const float* d_pts, int N, int dim, float* d_aos, void* stream) {
+int frnn_launch_transpose(const float* d_pts, int N, int dim, float* d_aos, const void* d_stats_ws,
+                          float* d_frows, float* d_fnorm, void* stream) {
     if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
     if (N > 0 && (!d_pts || !d_aos)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    return launch_status(frnn::launch_transpose(d_pts, N, dim, d_aos, (hipStream_t)stream),
+    if (d_stats_ws && (!d_frows || !d_fnorm)) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need both outputs");
+    return launch_status(frnn::launch_transpose(d_pts, N, dim, d_aos, d_stats_ws, d_frows, d_fnorm,
+                                                (hipStream_t)stream),
                          "transpose launch");
 }
 
-int frnn_launch_find_nbrs(const float* d_aos, const int* d_sorted_idx, const int* d_start, int N, int dim,
+int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float* d_fnorm,
+                          const int* d_sorted_idx, const int* d_start, const void* d_refine_ws, int N, int dim,
                           int K, const frnn_plan_t* plan, unsigned long long* d_lists, int list_cap,
                           unsigned long long* d_counters, void* stream) {
     if (!plan) return fail(FRNN_ERR_INVALID_ARGUMENT, "null plan");
@@ -475,15 +548,17 @@ int frnn_launch_find_nbrs(const float* d_aos, const int* d_sorted_idx, const int
     if (plan->path == FRNN_PATH_EMPTY || N == 0) return FRNN_OK;
     if (list_cap < frnn::list_capacity(K)) return fail(FRNN_ERR_INVALID_ARGUMENT, "list_cap too small");
     const bool grid = plan->path != FRNN_PATH_BRUTEFORCE;
-    if (!d_aos || !d_lists || (grid && (!d_sorted_idx || !d_start)))
+    if (!d_aos || !d_frows || !d_fnorm || !d_lists || (grid && (!d_sorted_idx || !d_start)))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
     if (grid && (plan->grid_dim < 1 || plan->grid_dim > 9 || plan->grid_dim > dim || plan->res < 1 ||
                  ipow_sat(plan->res, plan->grid_dim, (long long)4e18) != plan->cells ||
                  plan->cells > FRNN_MAX_CELLS))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "inconsistent grid plan");
     if (plan->rev_order && (!grid || dim != 3)) return fail(FRNN_ERR_INVALID_ARGUMENT, "reversed order is D=3 grid only");
-    return launch_status(frnn::launch_search(d_aos, d_sorted_idx, d_start, N, dim, K, *plan, d_lists,
-                                             list_cap, d_counters, (hipStream_t)stream),
+    if (d_refine_ws && frnn::refine_axes(*plan, dim) == 0)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "refinement tables given for a plan without refinement");
+    return launch_status(frnn::launch_search(d_aos, d_frows, d_fnorm, d_sorted_idx, d_start, d_refine_ws, N, dim,
+                                             K, *plan, d_lists, list_cap, d_counters, (hipStream_t)stream),
                          "search launch");
 }
 

@@ -23,6 +23,16 @@ __device__ __forceinline__ int bin_coord(float x, float inv_cell, int res) {
     return (int)f;
 }
 
+// Sub-bin of a refinement axis: floor((x - lo) * inv) clamped to [0, nb-1].
+// Monotone in x, so an interval of x maps onto an interval of sub-bins.
+__device__ __forceinline__ int sub_bin(float x, float lo, float inv, int nb) {
+    float t = (x - lo) * inv;
+    float f = floorf(t);
+    f = fmaxf(f, 0.0f);
+    f = fminf(f, (float)(nb - 1));
+    return (int)f;
+}
+
 // Total order on (d2, idx): non-negative fp32 bit patterns order like the
 // values, so one 64-bit compare ranks (d2, idx) lexicographically.
 __device__ __forceinline__ unsigned long long make_key(float d2, int idx) {
@@ -40,6 +50,16 @@ __device__ __forceinline__ int wave_min_i32(int v) {
 __device__ __forceinline__ int wave_max_i32(int v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_min_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;
 }
 __device__ __forceinline__ long long wave_sum_i64(long long v) {

@@ -16,9 +16,10 @@
 //     with conservative AABB trimming of the outer x cells;
 //   * candidates stream through in tiles of 32.  The distance tile
 //     32 candidates x 32 queries is one chain of v_mfma_f32_32x32x2f32 on the
-//     augmented vectors  a = [-2p', (1-c)|p'|^2, 1],  b = [q', 1, (1-c)|q'|^2]
-//     (p', q' centred on the first query of the wave), so the accumulator is a
-//     filter value F <= the exact distance plus a proven rounding bound;
+//     augmented vectors  a = [p', |p'|^2, 1],  b = [-2q', 1-c, (1-c)|q'|^2]
+//     (p', q' the rows centred on the input mean, precomputed with their norms
+//     by the reorder), so the accumulator is a filter value F <= the exact
+//     distance plus a proven rounding bound;
 //   * pairs with F below the query's threshold (plus a relative margin) are
 //     queued in LDS and re-evaluated 64 at a time with the reference's exact fp32
 //     distance order; accepted (d2, idx) keys go to a per-query candidate list;
@@ -41,17 +42,24 @@ namespace frnn {
 
 constexpr int kQB = 32;                      // queries per wave
 constexpr int kBatch = 64;                   // exact re-evaluations per batch
-constexpr int kQueueCap = kBatch + kQB * 32; // leftover batch + one full tile of hits
+constexpr int kQueueCap = kBatch + 4 * kWave;  // leftover batch + one register group of hits
 constexpr int kSortCap = 512;                // >= next_pow2(list_capacity(128))
+constexpr int kRing = 128;                   // pending candidate runs (<= 31 + 64 in use)
+constexpr int kMaxG = 9;
 
 struct SearchArgs {
     const float* pts;            // AoS rows, stride DS (sorted order for grids)
+    const float* frows;          // the same rows centred on the input mean: fl(x - mean)
+    const float* fnorm;          // squared norms of the centred rows
     const int* sorted_idx;       // sorted position -> original index (grid paths)
     const int* start;            // cells+1 exclusive cell offsets (grid paths)
+    const RefineInfo* ref;       // within-cell refinement, or nullptr
+    const int* bidx;             // big-cell index (exclusive scan of big flags)
+    const int* substart;         // sub-bin offsets of big cells
     unsigned long long* lists;   // [N][cap] candidate keys
     unsigned long long* counters;
     int N, K, cap, G, res;
-    float r2, cell, inv_cell;
+    float r2, cell, inv_cell, radius;
     float norm_scale;            // 1 - c_norm
     float thr_rel, thr_abs;      // filter threshold margin
     int nchunks, chunks_per_xcd;
@@ -119,17 +127,30 @@ __device__ __forceinline__ float exact_d2(const float* q, const float* __restric
     return acc;
 }
 
+// Small padded dimensions keep three waves per SIMD resident (register budget
+// 168); larger ones take what their operands need.
+template <int DS>
+struct WavesPerEU { static constexpr int value = DS <= 16 ? 3 : 1; };
+
 template <int DS, bool REV, bool BF>
-__global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DS>::value)))
+void search_kernel(SearchArgs a) {
     constexpr int HD = DS / 2;
+    constexpr bool PREFETCH = DS <= 32;
     __shared__ __align__(16) float s_q[kQB * DS];
-    __shared__ float s_o[DS];
     __shared__ int s_cnt[kQB];
     __shared__ unsigned long long s_thr[kQB];
     __shared__ int s_qn[kQueueCap];
     __shared__ int s_qpos[kQueueCap];
     __shared__ unsigned long long s_sort[kSortCap];
     __shared__ int s_qsize;
+    // candidate run ring: [start, start + (vend - vbeg)) of the sorted points,
+    // virtual stream positions [vbeg, vend), cell x and row-segment id
+    __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing], r_x[kRing], r_seg[kRing];
+    // current tile: candidate row -> sorted position, cell x, segment id
+    __shared__ int t_pos[32], t_x[32], t_seg[32];
+    __shared__ float s_blo[kMaxG], s_bhi[kMaxG];
+    __shared__ int s_rc[kMaxG];
 
     const int lane = threadIdx.x;
     const int n = lane & 31;
@@ -161,27 +182,31 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
     }
     if (lane == 0) s_qsize = 0;
     __syncthreads();
-    for (int d = lane; d < DS; d += kWave) s_o[d] = BF ? 0.0f : s_q[d];
-    __syncthreads();
-
-    // B operand: this lane's half of query n, centred, plus the norm column.
+    // B operand: this lane's half of query n's centred row, scaled by -2, plus
+    // the norm column.  Rows of a chunk are the sorted points q0..q0+31.
     float bop[HD + 1];
-    float qn2p = 0.0f;
+    float qn2 = 0.0f;
+    {
+        const float* fr = a.frows + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
 #pragma unroll
-    for (int j = 0; j < HD; ++j) {
-        const float v = s_q[n * DS + h * HD + j] - s_o[h * HD + j];
-        bop[j] = v;
-        qn2p = fmaf(v, v, qn2p);
+        for (int j = 0; j < HD; j += 2) {
+            const float2 v = *reinterpret_cast<const float2*>(fr + j);
+            bop[j] = -2.0f * v.x;
+            bop[j + 1] = -2.0f * v.y;
+        }
+        qn2 = a.fnorm[q0 + (qvalid ? n : 0)];
+        bop[HD] = (h == 0) ? a.norm_scale : qn2 * a.norm_scale;
     }
-    const float qn2 = qn2p + __shfl_xor(qn2p, 32);
-    bop[HD] = (h == 0) ? 1.0f : qn2 * a.norm_scale;
     if (!qvalid) {
 #pragma unroll
         for (int j = 0; j <= HD; ++j) bop[j] = 0.0f;
     }
     float thr_f = qvalid ? filter_threshold(a.r2, a) : -__builtin_huge_valf();
+    // Queries whose centred norm could overflow the filter always take the
+    // per-value (NaN-aware) hit test.
+    const bool robust_q = __ballot(qvalid && !(qn2 < 1.0e37f)) != 0;
 
-    long long c_shell = 0, c_hit = 0, c_acc = 0, c_ovf = 0;
+    long long c_shell = 0, c_hit = 0, c_acc = 0, c_ovf = 0, c_stream = 0;
 
     auto select_topk = [&](int qn, bool final_pass) {
         const int c = s_cnt[qn];
@@ -253,73 +278,180 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
         __syncthreads();
     };
 
-    auto process_run = [&](int A, int B, int lo, int hi) {
-        for (int t0 = A; t0 < B; t0 += 32) {
-            const int m = t0 + n;
-            const bool mvalid = m < B;
-            const float* src = a.pts + (size_t)(mvalid ? m : A) * DS + h * HD;
-            float aop[HD + 1];
-            float pn2p = 0.0f;
+    // ---- candidate stream -------------------------------------------------
+    int ring_head = 0, ring_tail = 0;   // absolute run indices (wave-uniform)
+    int v_total = 0, v_done = 0;        // virtual candidate positions (wave-uniform)
+    int jr = 0;                         // this lane's current run
+    int my_seg = -1;                    // row segment of this lane's query
+    int x_n = 0;                        // cell x of this lane's query
+
+    // Gather one tile of the stream into operand registers: the run lookup for
+    // stream position v0 + n, the centred row half and the norm column.
+    struct Tile {
+        float op[HD + 1];
+        int pos, x, seg, count;
+    };
+    auto gather = [&](int v0, int count, Tile& t) {
+        const int v = v0 + n;
+        const bool mvalid = n < count;
+        t.count = count;
+        t.pos = 0;
+        t.x = 0;
+        t.seg = -1;
+        if (mvalid) {
+            if (jr < ring_tail) jr = ring_tail;
+            while (r_vend[jr & (kRing - 1)] <= v) ++jr;
+            const int j = jr & (kRing - 1);
+            t.pos = r_start[j] + (v - r_vbeg[j]);
+            t.x = r_x[j];
+            t.seg = r_seg[j];
+        }
+        const float* fr = a.frows + (size_t)t.pos * DS + h * HD;
 #pragma unroll
-            for (int j = 0; j < HD; j += 2) {
-                const float2 v = *reinterpret_cast<const float2*>(src + j);
-                const float d0 = v.x - s_o[h * HD + j];
-                const float d1 = v.y - s_o[h * HD + j + 1];
-                aop[j] = -2.0f * d0;
-                aop[j + 1] = -2.0f * d1;
-                pn2p = fmaf(d0, d0, pn2p);
-                pn2p = fmaf(d1, d1, pn2p);
+        for (int j = 0; j < HD; j += 2) {
+            const float2 vv = *reinterpret_cast<const float2*>(fr + j);
+            t.op[j] = vv.x;
+            t.op[j + 1] = vv.y;
+        }
+        t.op[HD] = (h == 0) ? (mvalid ? a.fnorm[t.pos] : 3.0e38f) : 1.0f;
+    };
+
+    // MFMA filter of one gathered tile: the 32 x 32 accumulator of filter values.
+    auto mfma_tile = [&](const Tile& t) {
+        floatx16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j <= HD; ++j)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(t.op[j], bop[j], acc, 0, 0, 0);
+        return acc;
+    };
+
+    // Queue the tile's hits (filter value below the query's threshold, candidate
+    // inside the query's shell) for exact re-evaluation.
+    auto hits_tile = [&](const Tile& t, const floatx16& acc) {
+        if (h == 0) {
+            t_pos[n] = t.pos;
+            t_x[n] = t.x;
+            t_seg[n] = t.seg;
+        }
+        const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(t.op[HD] < 1.0e37f)) != 0);
+        // per group of four accumulator registers: does this lane hold a hit?
+        bool gh[4];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            if (!robust) {
+                const float m = fminf(fminf(acc[4 * g4], acc[4 * g4 + 1]), fminf(acc[4 * g4 + 2], acc[4 * g4 + 3]));
+                gh[g4] = m < thr_f;
+            } else {
+                gh[g4] = !(acc[4 * g4] >= thr_f) || !(acc[4 * g4 + 1] >= thr_f) ||
+                         !(acc[4 * g4 + 2] >= thr_f) || !(acc[4 * g4 + 3] >= thr_f);
             }
-            const float pn2 = pn2p + __shfl_xor(pn2p, 32);
-            aop[HD] = (h == 0) ? (mvalid ? pn2 * a.norm_scale : 3.0e38f) : 1.0f;
-
-            floatx16 acc;
+        }
+        if (__ballot(gh[0] || gh[1] || gh[2] || gh[3]) == 0) return;
+        __syncthreads();
+        // four groups of four registers: at most 4 hits per lane per group, so
+        // the queue never exceeds 63 + 256 entries
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        for (int g4 = 0; g4 < 4; ++g4) {
+            if (__ballot(gh[g4]) == 0) continue;
+            if (gh[g4]) {
 #pragma unroll
-            for (int j = 0; j <= HD; ++j)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(aop[j], bop[j], acc, 0, 0, 0);
-
-            bool any = false;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) any |= !(acc[r] >= thr_f);
-            if (__ballot(any)) {
-                if (any) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        if (!(acc[r] >= thr_f)) {
-                            // 32x32 accumulator layout: lane (n, h), register r holds
-                            // row 8*(r/4) + 4*h + r%4 (the candidate) of column n.
-                            const int pos = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                            if (pos >= lo && pos < hi) {
-                                const int s = atomicAdd(&s_qsize, 1);
-                                if (s < kQueueCap) {
-                                    s_qn[s] = n;
-                                    s_qpos[s] = pos;
-                                } else {
-                                    ++c_ovf;
-                                }
-                                ++c_hit;
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int r = 4 * g4 + rr;
+                    if (!(acc[r] >= thr_f)) {
+                        // 32x32 accumulator layout: lane (n, h), register r holds
+                        // row 8*(r/4) + 4*h + r%4 (the candidate) of column n.
+                        const int row = 8 * g4 + 4 * h + rr;
+                        const int tseg = t_seg[row];
+                        const bool member = BF ? (tseg >= 0)
+                                               : (tseg == my_seg && abs(t_x[row] - x_n) <= 1);
+                        if (member && qvalid) {
+                            const int s = atomicAdd(&s_qsize, 1);
+                            if (s < kQueueCap) {
+                                s_qn[s] = n;
+                                s_qpos[s] = t_pos[row];
+                            } else {
+                                ++c_ovf;
                             }
+                            ++c_hit;
                         }
                     }
                 }
-                __syncthreads();
-                int qs = min(s_qsize, kQueueCap);
-                while (qs >= kBatch) {
-                    process_batch(qs - kBatch, kBatch);
-                    qs -= kBatch;
-                }
+            }
+            __syncthreads();
+            int qs = min(s_qsize, kQueueCap);
+            while (qs >= kBatch) {
+                process_batch(qs - kBatch, kBatch);
+                qs -= kBatch;
             }
         }
     };
 
+    // Stream the available candidates: each tile's MFMA chain is issued first,
+    // then (PREFETCH) the next tile's rows are gathered, so those loads are in
+    // flight while the MFMAs run and the current tile's hits are handled.
+    auto consume = [&](bool final_pass) {
+        int avail = v_total - v_done;
+        if (!(avail >= 32 || (final_pass && avail > 0))) return;
+        Tile cur;
+        gather(v_done, min(32, avail), cur);
+        while (true) {
+            const int vn = v_done + cur.count;
+            const int an = v_total - vn;
+            const bool has_next = an >= 32 || (final_pass && an > 0);
+            const floatx16 acc = mfma_tile(cur);
+            Tile nxt;
+            if constexpr (PREFETCH) {
+                if (has_next) gather(vn, min(32, an), nxt);
+            }
+            hits_tile(cur, acc);
+            if (h == 0 && n == 0) c_stream += cur.count;
+            v_done = vn;
+            while (ring_tail < ring_head && r_vend[ring_tail & (kRing - 1)] <= v_done) ++ring_tail;
+            if (!has_next) break;
+            if constexpr (PREFETCH) {
+                cur = nxt;
+            } else {
+                gather(vn, min(32, an), cur);
+            }
+        }
+    };
+
+    // Append at most one run per lane (in lane order) to the ring.
+    auto append_runs = [&](int start, int len, int x, int seg) {
+        const bool has = len > 0;
+        const unsigned long long mask = __ballot(has);
+        if (mask == 0) return;
+        int incl = has ? len : 0;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        const int total = __shfl(incl, kWave - 1);
+        const int k = __popcll(mask & ((1ull << lane) - 1ull));
+        if (has) {
+            const int slot = (ring_head + k) & (kRing - 1);
+            r_start[slot] = start;
+            r_vbeg[slot] = v_total + incl - len;
+            r_vend[slot] = v_total + incl;
+            r_x[slot] = x;
+            r_seg[slot] = seg;
+        }
+        ring_head += __popcll(mask);
+        v_total += total;
+        __syncthreads();
+    };
+
     if constexpr (BF) {
         if (qvalid && h == 0) c_shell += a.N;
-        process_run(0, a.N, 0, qvalid ? a.N : 0);
+        my_seg = qvalid ? 0 : -1;
+        append_runs(0, lane == 0 ? a.N : 0, 0, 0);
+        consume(false);
     } else {
         const float* qrow = s_q + n * DS;
-        int x_n = bin_coord(qrow[0], a.inv_cell, a.res);
+        x_n = bin_coord(qrow[0], a.inv_cell, a.res);
         int row_n = 0;
         {
             int mul = 1;
@@ -332,69 +464,142 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
         int nrows = 1;
         for (int d = 1; d < a.G; ++d) nrows *= 3;
         const float keep = 0.9999847412109375f;   // 1 - 2^-16
+        const float eps = 4.76837158203125e-07f;  // 2^-21
+        const int L = a.ref ? a.ref->L : 0;
 
-        int seg = 0;
+        int seg = 0, seg_id = 0;
         while (seg < nq) {
             const int R = __shfl(row_n, seg);
             const bool in_seg = (row_n == R);
+            if (in_seg) my_seg = seg_id;
             const int xlo = wave_min_i32(in_seg ? x_n : 0x7fffffff);
             const int xhi = wave_max_i32(in_seg ? x_n : -1);
             const int seg_end = __popcll(__ballot(row_n <= R) & 0xffffffffull);
-
-            for (int t = 0; t < nrows; ++t) {
-                int tt = t, Rt = R, Rn = 0, mul = 1;
-                bool ok = true;
-                float lbr = 0.0f;
-                for (int d = 1; d < a.G; ++d) {
-                    const int rc = Rt % a.res;
-                    Rt /= a.res;
-                    const int cc = rc + (tt % 3) - 1;
-                    tt /= 3;
-                    ok = ok && cc >= 0 && cc < a.res;
-                    Rn += cc * mul;
-                    mul *= a.res;
-                    const float gd = axis_gap(qrow[d], cc, a.res, a.cell);
-                    lbr = fmaf(gd, gd, lbr);
+            // segment bounding box on the gridded axes and the largest threshold
+            for (int d = 0; d < a.G; ++d) {
+                const float qd = qrow[d];
+                const float lo = wave_min_f32(in_seg ? qd : __builtin_huge_valf());
+                const float hi = wave_max_f32(in_seg ? qd : -__builtin_huge_valf());
+                if (lane == 0) { s_blo[d] = lo; s_bhi[d] = hi; }
+            }
+            if (lane == 0) {
+                int Rt = R;
+                for (int d = 1; d < a.G; ++d) { s_rc[d] = Rt % a.res; Rt /= a.res; }
+            }
+            const float thr_seg = wave_max_f32(in_seg ? key_d2(s_thr[n]) : -__builtin_huge_valf());
+            // refinement windows: every candidate within the radius of a
+            // segment query has its axis coordinate inside [w_lo, w_hi]
+            int qlo0 = 0, qhi0 = 0, qlo1 = 0, qhi1 = 0, nb2 = 1;
+            if (L > 0) {
+                const RefineInfo* rf = a.ref;
+                nb2 = rf->nb2;
+                const float x0v = qrow[rf->axis0];
+                const float lo0 = wave_min_f32(in_seg ? x0v : __builtin_huge_valf());
+                const float hi0 = wave_max_f32(in_seg ? x0v : -__builtin_huge_valf());
+                const float h0 = a.radius * 1.000030517578125f + 2.384185791015625e-07f * (fabsf(lo0) + fabsf(hi0));
+                qlo0 = sub_bin(lo0 - h0, rf->lo0, rf->inv0, rf->nb1);
+                qhi0 = sub_bin(hi0 + h0, rf->lo0, rf->inv0, rf->nb1);
+                if (L > 1) {
+                    const float x1v = qrow[rf->axis1];
+                    const float lo1 = wave_min_f32(in_seg ? x1v : __builtin_huge_valf());
+                    const float hi1 = wave_max_f32(in_seg ? x1v : -__builtin_huge_valf());
+                    const float h1 = a.radius * 1.000030517578125f + 2.384185791015625e-07f * (fabsf(lo1) + fabsf(hi1));
+                    qlo1 = sub_bin(lo1 - h1, rf->lo1, rf->inv1, rf->nb2);
+                    qhi1 = sub_bin(hi1 + h1, rf->lo1, rf->inv1, rf->nb2);
                 }
-                if (!ok) continue;
-                const int base = Rn * a.res;
-                const int A = a.start[base + max(xlo - 1, 0)];
-                const int B = a.start[base + min(xhi + 1, a.res - 1) + 1];
-                if (A >= B) continue;
+            }
+            __syncthreads();
 
-                int lo = 0, hi = 0;
-                if (in_seg) {
-                    const int xl = max(x_n - 1, 0);
-                    const int xh = min(x_n + 1, a.res - 1);
-                    lo = a.start[base + xl];
-                    hi = a.start[base + xh + 1];
-                    if (h == 0) c_shell += hi - lo;
-                    const float thrE = key_d2(s_thr[n]);
-                    if (lbr * keep > thrE) {
-                        lo = hi;
-                    } else {
-                        if (xl < x_n) {
-                            const float gx = axis_gap(qrow[0], xl, a.res, a.cell);
-                            if (fmaf(gx, gx, lbr) * keep > thrE) lo = a.start[base + x_n];
-                        }
-                        if (xh > x_n) {
-                            const float gx = axis_gap(qrow[0], xh, a.res, a.cell);
-                            if (fmaf(gx, gx, lbr) * keep > thrE) hi = a.start[base + x_n + 1];
+            if (a.counters && in_seg && h == 0) {
+                for (int t = 0; t < nrows; ++t) {
+                    int tt = t, Rn = 0, mul = 1;
+                    bool ok = true;
+                    for (int d = 1; d < a.G; ++d) {
+                        const int cc = s_rc[d] + (tt % 3) - 1;
+                        tt /= 3;
+                        ok = ok && cc >= 0 && cc < a.res;
+                        Rn += cc * mul;
+                        mul *= a.res;
+                    }
+                    if (!ok) continue;
+                    const int base = Rn * a.res;
+                    c_shell += a.start[base + min(x_n + 1, a.res - 1) + 1] - a.start[base + max(x_n - 1, 0)];
+                }
+            }
+
+            const int xa = max(xlo - 1, 0);
+            const int nx = min(xhi + 1, a.res - 1) - xa + 1;
+            const int nq1 = L > 0 ? max(qhi0 - qlo0 + 1, 0) : 1;
+            const int NI = nx * nrows * nq1;
+            for (int ib = 0; ib < NI; ib += kWave) {
+                const int item = ib + lane;
+                int rs = 0, rl = 0, rxv = 0;
+                if (item < NI) {
+                    const int q1i = item % nq1;
+                    const int rest = item / nq1;
+                    const int x = xa + rest % nx;
+                    int tt = rest / nx, Rn = 0, mul = 1;
+                    bool ok = true;
+                    for (int d = 1; d < a.G; ++d) {
+                        const int cc = s_rc[d] + (tt % 3) - 1;
+                        tt /= 3;
+                        ok = ok && cc >= 0 && cc < a.res;
+                        Rn += cc * mul;
+                        mul *= a.res;
+                    }
+                    rxv = x;
+                    if (ok) {
+                        const int c = x + a.res * Rn;
+                        const int cs = a.start[c];
+                        const int ce = a.start[c + 1];
+                        if (ce > cs) {
+                            // conservative AABB test of the whole cell against the
+                            // segment's queries
+                            float lb = 0.0f;
+                            int cd = c;
+                            for (int d = 0; d < a.G; ++d) {
+                                const int ci = cd % a.res;
+                                cd /= a.res;
+                                float gap = 0.0f;
+                                if (ci > 0) {
+                                    const float lo = (float)ci * a.cell;
+                                    gap = fmaxf(gap, (lo - s_bhi[d]) - eps * (fabsf(lo) + fabsf(s_bhi[d])));
+                                }
+                                if (ci < a.res - 1) {
+                                    const float hi = (float)(ci + 1) * a.cell;
+                                    gap = fmaxf(gap, (s_blo[d] - hi) - eps * (fabsf(hi) + fabsf(s_blo[d])));
+                                }
+                                lb = fmaf(gap, gap, lb);
+                            }
+                            if (!(lb * keep > thr_seg)) {
+                                if (L > 0 && ce - cs >= kBigCell) {
+                                    const int q1 = qlo0 + q1i;
+                                    const size_t sb = (size_t)a.bidx[c] * kSubBins;
+                                    const int s0 = a.substart[sb];
+                                    const int sl = a.substart[sb + q1 * nb2 + qlo1];
+                                    const int sh = a.substart[sb + q1 * nb2 + qhi1 + 1];
+                                    rs = cs + (sl - s0);
+                                    rl = sh - sl;
+                                } else if (q1i == 0) {
+                                    rs = cs;
+                                    rl = ce - cs;
+                                }
+                            }
                         }
                     }
                 }
-                const int wlo = wave_min_i32(lo < hi ? lo : 0x7fffffff);
-                const int whi = wave_max_i32(lo < hi ? hi : -1);
-                if (wlo >= whi) continue;
-                process_run(wlo, whi, lo, hi);
+                append_runs(rs, rl, rxv, seg_id);
+                consume(false);
             }
             seg = seg_end;
+            ++seg_id;
         }
     }
+    consume(true);
 
     __syncthreads();
     {
-        const int qs = s_qsize;
+        const int qs = min(s_qsize, kQueueCap);
         if (qs > 0) process_batch(0, qs);
     }
     for (int qn = 0; qn < nq; ++qn) select_topk(qn, true);
@@ -403,12 +608,14 @@ __global__ __launch_bounds__(64) void search_kernel(SearchArgs a) {
         const long long s0 = wave_sum_i64(c_shell);
         const long long s1 = wave_sum_i64(c_hit);
         const long long s2 = wave_sum_i64(c_acc);
-        const long long s3 = wave_sum_i64(c_ovf);
+        const long long s3 = wave_sum_i64(c_stream) * kQB;
+        const long long s4 = wave_sum_i64(c_ovf);
         if (lane == 0) {
             atomicAdd(&a.counters[0], (unsigned long long)s0);
             atomicAdd(&a.counters[1], (unsigned long long)s1);
             atomicAdd(&a.counters[2], (unsigned long long)s2);
-            if (s3) atomicAdd(&a.counters[3], (unsigned long long)s3);
+            atomicAdd(&a.counters[3], (unsigned long long)s3);
+            if (s4) atomicAdd(&a.counters[4], (unsigned long long)s4);
         }
     }
 }
@@ -424,15 +631,17 @@ static void launch_ds(const SearchArgs& a, bool bf, hipStream_t s) {
     else launch_one<DS, false, false>(a, s);
 }
 
-int launch_search(const float* aos, const int* sorted_idx, const int* start, int N, int D, int K,
-                  const frnn_plan_t& plan, unsigned long long* lists, int cap,
-                  unsigned long long* counters, hipStream_t s) {
+int launch_search(const float* aos, const float* frows, const float* fnorm, const int* sorted_idx,
+                  const int* start, const void* refine_ws, int N, int D, int K, const frnn_plan_t& plan,
+                  unsigned long long* lists, int cap, unsigned long long* counters, hipStream_t s) {
     if (N <= 0) return 0;
     const bool bf = plan.path == FRNN_PATH_BRUTEFORCE;
     if (!bf && (plan.grid_dim < 1 || plan.grid_dim > 9)) return 1;
-    if (cap < list_capacity(K) || K > FRNN_MAX_K) return 1;
+    if (cap < list_capacity(K) || K > FRNN_MAX_K || !frows || !fnorm) return 1;
     SearchArgs a{};
     a.pts = aos;
+    a.frows = frows;
+    a.fnorm = fnorm;
     a.sorted_idx = sorted_idx;
     a.start = start;
     a.lists = lists;
@@ -446,6 +655,14 @@ int launch_search(const float* aos, const int* sorted_idx, const int* start, int
     a.inv_cell = plan.inv_cell;
     const int DS = aos_stride(D);
     a.cell = bf ? 1.0f : plan.cell_size;
+    a.radius = plan.cell_size;
+    if (refine_ws && !bf) {
+        const RefineLayout L = refine_layout(N, D, plan.cells);
+        const char* base = static_cast<const char*>(refine_ws);
+        a.ref = reinterpret_cast<const RefineInfo*>(base + L.info);
+        a.bidx = reinterpret_cast<const int*>(base + L.bidx);
+        a.substart = reinterpret_cast<const int*>(base + L.substart);
+    }
     const double u = 5.9604644775390625e-08;   // 2^-24
     a.norm_scale = (float)(1.0 - (6.0 * DS + 32.0) * u);
     a.thr_rel = (float)(2.0 * (DS + 8.0) * u);

@@ -24,9 +24,9 @@ __all__ = ["FRNNEngine", "plan", "FRNNError", "LIB_PATH", "MAX_K", "MAX_DIM", "M
 MAX_K = 128
 MAX_DIM = 128
 MAX_CELLS = 1_000_000
-NUM_STAGES = 6
-NUM_COUNTERS = 3
-STAGE_NAMES = ("zero_fill", "bin_count", "scan", "reorder", "search", "unpermute")
+NUM_STAGES = 8
+NUM_COUNTERS = 4
+STAGE_NAMES = ("zero_fill", "bin_count", "stats", "scan", "refine", "reorder", "search", "unpermute")
 PATH_NAMES = {-1: "empty", 0: "bruteforce", 1: "grid_full", 2: "grid_first"}
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -86,10 +86,14 @@ def _load():
         "frnn_engine_counters": ([vp, vp, i32], i32),
         "frnn_launch_bin_count": ([vp, i32, i32, i32, f32, i64, vp, vp, vp, vp], i32),
         "frnn_launch_exclusive_scan": ([vp, i32, vp, vp, vp], i32),
-        "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, vp, vp], i32),
-        "frnn_launch_transpose": ([vp, i32, i32, vp, vp], i32),
-        "frnn_launch_find_nbrs": ([vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan), vp, i32,
-                                   vp, vp], i32),
+        "frnn_stats_workspace_bytes": ([i32], i64),
+        "frnn_launch_point_stats": ([vp, i32, i32, vp, vp], i32),
+        "frnn_refine_workspace_bytes": ([i32, i32, ctypes.POINTER(_Plan)], i64),
+        "frnn_launch_refine": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp, vp, vp, vp], i32),
+        "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, vp], i32),
+        "frnn_launch_transpose": ([vp, i32, i32, vp, vp, vp, vp, vp], i32),
+        "frnn_launch_find_nbrs": ([vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan), vp,
+                                   i32, vp, vp], i32),
         "frnn_launch_unpermute": ([vp, i32, vp, i32, i32, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
@@ -113,9 +117,19 @@ def _check(status, what=""):
 
 def plan(N, dim, K, radius):
     """The reference's auto-dispatch decision for (N, dim, K, radius) as a dict."""
+    return _plan_struct(N, dim, K, radius).as_dict()
+
+
+def _plan_struct(N, dim, K, radius):
     p = _Plan()
     _check(_load().frnn_make_plan(int(N), int(dim), int(K), float(radius), ctypes.byref(p)), "plan")
-    return p.as_dict()
+    return p
+
+
+def refine_workspace_bytes(N, dim, K, radius):
+    """Bytes of the within-cell refinement workspace for this problem (0: none)."""
+    return int(_load().frnn_refine_workspace_bytes(int(N), int(dim),
+                                                   ctypes.byref(_plan_struct(N, dim, K, radius))))
 
 
 def aos_stride(dim):
@@ -214,7 +228,8 @@ class FRNNEngine:
         c = np.zeros(NUM_COUNTERS, dtype=np.int64)
         _check(_load().frnn_engine_counters(self._handle(), c.ctypes.data_as(ctypes.c_void_p),
                                             NUM_COUNTERS), "counters")
-        return {"shell_candidates": int(c[0]), "filter_hits": int(c[1]), "accepted": int(c[2])}
+        return {"shell_candidates": int(c[0]), "filter_hits": int(c[1]), "accepted": int(c[2]),
+                "streamed_pairs": int(c[3])}
 
     def close(self):
         h = getattr(self, "_h", None)

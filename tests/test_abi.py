@@ -104,8 +104,21 @@ def test_launch_seam_rejects_bad_geometry_without_touching_the_device():
     p = frnn_cuda._Plan()
     assert L.frnn_make_plan(100000, 12, 32, ctypes.c_float(0.0345), ctypes.byref(p)) == 0
     p.cells = 5
-    assert L.frnn_launch_find_nbrs(None, None, None, 100000, 12, 32, ctypes.byref(p), None, 128,
-                                   None, None) == 1
+    assert L.frnn_launch_find_nbrs(None, None, None, None, None, None, 100000, 12, 32, ctypes.byref(p),
+                                   None, 128, None, None) == 1
+    assert L.frnn_launch_refine(None, 10, 12, None, None, None, None, None, None, None) == 1
+    assert L.frnn_launch_reorder(None, 10, 3, None, None, None, None, None, 0, None, None, None, None, None,
+                                 None, None) == 1
+    assert L.frnn_launch_point_stats(None, 10, 3, None, None) == 1
+    assert L.frnn_stats_workspace_bytes(0) == -1 and L.frnn_stats_workspace_bytes(16) > 0
+
+
+def test_refine_workspace_sizes():
+    # refinement only for first-coordinate plans with dim > grid_dim
+    assert frnn_cuda.refine_workspace_bytes(100000, 12, 32, 0.0345) > 0     # grid_first g=4
+    assert frnn_cuda.refine_workspace_bytes(100000, 3, 16, 0.1) == 0        # full-D grid
+    assert frnn_cuda.refine_workspace_bytes(200000, 128, 128, 12.96) == 0   # brute force
+    assert frnn_cuda.refine_workspace_bytes(100000, 4, 8, 0.02) > 0         # grid_first g=3, one axis
 
 
 @pytest.mark.skipif(gpu_visible(), reason="checks the no-device error path")

@@ -9,6 +9,7 @@ import ctypes
 import numpy as np
 import pytest
 
+import exact_fp32 as E
 import frnn_cuda
 import frnn_oracle as O
 import frnn_workloads as W
@@ -37,8 +38,8 @@ def _build(X, g, res, inv):
     sidx = t.empty(N, dtype=t.int32, device="cuda:0")
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.full((N * ds,), float("nan"), dtype=t.float32, device="cuda:0")
-    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(sidx), vp(inv_p),
-                                 vp(aos), None) == 0
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), None, cells,
+                                 vp(sidx), vp(inv_p), vp(aos), None, None, None, None) == 0
     t.cuda.synchronize()
     return {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start,
                                                   sidx=sidx, inv=inv_p, aos=aos).items()}
@@ -107,3 +108,97 @@ def test_bin_count_out_of_domain_and_nan():
     out = _build(X, 2, res, inv)
     assert np.array_equal(out["cell_of"], O.bin_cells(X, 2, res, np.float32(inv)))
     assert list(out["cell_of"][:3]) == [0 + 4 * 2, 2 + 4 * 3, 3 + 4 * 3]
+
+
+def _sub_bins(x, lo, inv, nb):
+    t = (x.astype(np.float32) - np.float32(lo)).astype(np.float32) * np.float32(inv)
+    f = np.fmin(np.fmax(np.floor(t.astype(np.float32)), np.float32(0)), np.float32(nb - 1))
+    return f.astype(np.int64)
+
+
+@pytest.mark.parametrize("name,N", [("metric", 300_000), ("C3", 300_000)])
+def test_refinement_orders_big_cells(name, N):
+    """Within-cell refinement: axis choice, sub-bin order inside big cells, and the
+    usual permutation / cell-order / row-copy invariants of the reorder."""
+    t = torch()
+    w = W.config(name, N=N)
+    plan = frnn_cuda._plan_struct(N, w.D, w.K, w.radius)
+    assert plan.path == 2 and plan.grid_dim == 4
+    g, res, cells = plan.grid_dim, plan.res, plan.cells
+    L = frnn_cuda._load()
+    log(f"refinement {name} N={N} res={res}")
+    d = device_soa(w.X)
+    cell_of = t.empty(N, dtype=t.int32, device="cuda:0")
+    rank = t.empty(N, dtype=t.int32, device="cuda:0")
+    cnt = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
+    assert L.frnn_launch_bin_count(vp(d), N, g, res, ctypes.c_float(plan.inv_cell), cells, vp(cell_of),
+                                   vp(rank), vp(cnt), None) == 0
+    start = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
+    part = t.empty(frnn_cuda.scan_partials_count(cells + 1), dtype=t.int32, device="cuda:0")
+    assert L.frnn_launch_exclusive_scan(vp(cnt), cells + 1, vp(start), vp(part), None) == 0
+    sws = t.zeros(L.frnn_stats_workspace_bytes(w.D), dtype=t.uint8, device="cuda:0")
+    assert L.frnn_launch_point_stats(vp(d), N, w.D, vp(sws), None) == 0
+    wsb = L.frnn_refine_workspace_bytes(N, w.D, ctypes.byref(plan))
+    assert wsb > 0
+    ws = t.zeros(wsb, dtype=t.uint8, device="cuda:0")
+    assert L.frnn_launch_refine(vp(d), N, w.D, ctypes.byref(plan), vp(cell_of), vp(cnt), vp(rank),
+                                vp(sws), vp(ws), None) == 0
+    ds = frnn_cuda.aos_stride(w.D)
+    sidx = t.empty(N, dtype=t.int32, device="cuda:0")
+    inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
+    aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
+    frows = t.empty(N * ds, dtype=t.float32, device="cuda:0")
+    fnorm = t.empty(N, dtype=t.float32, device="cuda:0")
+    assert L.frnn_launch_reorder(vp(d), N, w.D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
+                                 vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), vp(fnorm), None) == 0
+    t.cuda.synchronize()
+    head = ws[:64].cpu().numpy()
+    ints, flts = head.view(np.int32), head.view(np.float32)
+    axes, nb1, nb2, ax0, ax1 = (int(v) for v in ints[:5])
+    lo0, lo1, inv0, inv1 = (float(v) for v in flts[5:9])
+    var = w.X[:, g:].astype(np.float64).var(0)
+    order = np.argsort(-var, kind="stable")
+    assert axes == 2 and nb1 * nb2 == 1024
+    assert (ax0, ax1) == (g + order[0], g + order[1])
+    sidx, inv_p = sidx.cpu().numpy(), inv_p.cpu().numpy()
+    cnt = cnt.cpu().numpy()[:cells]
+    cells_of = O.bin_cells(w.X, g, res, np.float32(plan.inv_cell))
+    assert np.array_equal(np.sort(sidx), np.arange(N))
+    assert np.array_equal(sidx[inv_p], np.arange(N))
+    cs = cells_of[sidx]
+    assert np.all(np.diff(cs) >= 0)
+    rows = aos.cpu().numpy().reshape(N, ds)
+    assert np.array_equal(rows[:, :w.D], w.X[sidx])
+    key = _sub_bins(w.X[sidx, ax0], lo0, inv0, nb1) * nb2 + _sub_bins(w.X[sidx, ax1], lo1, inv1, nb2)
+    # filter rows: fl(x - mean) and their sequential-fma squared norms
+    mean = sws[:16 * w.D].cpu().numpy().view(np.float32).reshape(w.D, 4)[:, 0]
+    fr = frows.cpu().numpy().reshape(N, ds)
+    assert np.array_equal(fr[:, :w.D], (w.X[sidx] - mean[None, :]).astype(np.float32))
+    assert np.all(fr[:, w.D:] == 0)
+    assert np.array_equal(fnorm.cpu().numpy(), E.dist2(fr, np.zeros_like(fr), 0))
+    big = cnt[cs] >= 256
+    assert big.mean() > 0.5                      # most points live in refined cells here
+    same_cell = np.concatenate([[False], cs[1:] == cs[:-1]])
+    step = np.concatenate([[0], np.diff(key)])
+    assert np.all(step[same_cell & big] >= 0)
+
+
+def test_point_stats():
+    t = torch()
+    rs = np.random.RandomState(2)
+    X = (rs.standard_normal((100_003, 7)) * [1, 2, 3, 0.5, 10, 1e-3, 4] + [0, 1, -2, 5, 0, 1e3, 0]).astype(np.float32)
+    X[5, 3] = np.nan                              # NaN column: mean falls back to 0, variance -1
+    d = device_soa(X)
+    L = frnn_cuda._load()
+    sws = t.zeros(L.frnn_stats_workspace_bytes(7), dtype=t.uint8, device="cuda:0")
+    assert L.frnn_launch_point_stats(vp(d), len(X), 7, vp(sws), None) == 0
+    t.cuda.synchronize()
+    st = sws[:16 * 7].cpu().numpy().view(np.float32).reshape(7, 4)
+    X64 = X.astype(np.float64)
+    for dd in range(7):
+        if dd == 3:
+            assert st[dd, 0] == 0 and st[dd, 1] == -1
+            continue
+        assert abs(st[dd, 0] - X64[:, dd].mean()) <= 1e-6 * (1 + abs(X64[:, dd].mean()))
+        assert abs(st[dd, 1] - X64[:, dd].var()) <= 1e-5 * X64[:, dd].var()
+        assert st[dd, 2] == X[:, dd].min() and st[dd, 3] == X[:, dd].max()
