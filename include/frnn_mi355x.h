@@ -68,14 +68,26 @@ typedef struct frnn_dim_stat {
 } frnn_dim_stat_t;
 
 /* Within-cell refinement descriptor; a refinement workspace starts with it.
- * Sub-bin of coordinate x on axis k: clamp(floor((x - lo_k) * inv_k), 0, bins_k - 1). */
+ * Direction k (0 or 1) projects point x as the sequential fp32 fma chain
+ *   s = 0;  s = fmaf(w_k[t], fl(x[coord[t]] - mean[t]), s)  for t = 0..terms-1
+ * and its sub-bin is clamp(floor((s - lo_k) * inv_k), 0, bins_k - 1).  The
+ * weights are the top principal directions of the non-grid coordinates
+ * (norm < 1); margin bounds |computed s - exact w_k.(x - mean)| over every
+ * finite input point, so two points within the radius have projections
+ * closer than radius * (1 + 2^-15) + 2 * margin. */
+#define FRNN_REFINE_TERMS 32
 typedef struct frnn_refine_info {
-    int axes;          /* number of refinement axes (1 or 2) */
-    int bins0, bins1;  /* sub-bins per axis; bins0 * bins1 == 1024 */
-    int axis0, axis1;  /* coordinates used (highest variance first) */
-    float lo0, lo1;
-    float inv0, inv1;
+    int axes;          /* number of refinement directions (1 or 2) */
+    int bins0, bins1;  /* sub-bins per direction; bins0 * bins1 == 1024 */
+    int terms;         /* coordinates per projection, <= FRNN_REFINE_TERMS */
+    float lo0, lo1;    /* bin origin per direction */
+    float inv0, inv1;  /* bins per unit per direction (0: a single bin) */
+    float margin;      /* projection rounding bound */
     int reserved[7];
+    int coord[FRNN_REFINE_TERMS];   /* term coordinates, highest variance first */
+    float mean[FRNN_REFINE_TERMS];  /* term centres (the point-statistics means) */
+    float w0[FRNN_REFINE_TERMS];    /* direction 0 weights */
+    float w1[FRNN_REFINE_TERMS];    /* direction 1 weights */
 } frnn_refine_info_t;
 
 /* ---- host-only helpers (no HIP call) ------------------------------------ */
@@ -170,9 +182,10 @@ int frnn_launch_point_stats(const float* d_points_soa, int N, int dim, void* d_s
 /* Within-cell refinement (no reference counterpart: the reference's within-cell
  * order is atomic arrival order, insert_points.cu:156-158, so any order is
  * admissible).  For first-coordinate plans with dim > grid_dim, cells holding
- * at least 256 points get 1024 sub-bins on the two highest-variance non-grid
- * axes (from d_stats_ws); d_rank of their points is replaced by the sub-bin
- * arrival slot.  Needs frnn_refine_workspace_bytes() bytes at d_ws (0 bytes:
+ * at least 256 points get 1024 sub-bins on the projections onto the two
+ * principal directions of the (up to 32 highest-variance) non-grid
+ * coordinates (frnn_refine_info_t; statistics from d_stats_ws); d_rank of
+ * their points is replaced by the sub-bin arrival slot.  Needs frnn_refine_workspace_bytes() bytes at d_ws (0 bytes:
  * plan has no refinement, nothing to launch).  Run after the scan, before the
  * reorder. */
 long long frnn_refine_workspace_bytes(int N, int dim, const frnn_plan_t* plan);

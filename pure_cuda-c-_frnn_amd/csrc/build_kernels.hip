@@ -158,13 +158,14 @@ __device__ __forceinline__ void write_rows(const float* __restrict__ pts, int N,
 
 // One thread per point: SoA reads are coalesced per axis; the AoS row store
 // is ds/4 16-byte vector stores to one contiguous row.  Points of big cells go
-// to their sub-bin's range of the cell (within-cell refinement order).
+// to their sub-bin's range of the cell (within-cell refinement order, sub-bin
+// key from sub_count_kernel).
 __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ pts, int N, int D, int ds,
                                                       const int* __restrict__ cell_of,
                                                       const int* __restrict__ rank,
                                                       const int* __restrict__ start,
                                                       const int* __restrict__ cnt,
-                                                      const RefineInfo* __restrict__ ref,
+                                                      const int* __restrict__ subkey,
                                                       const int* __restrict__ bidx,
                                                       const int* __restrict__ substart,
                                                       int* __restrict__ sorted_idx,
@@ -177,12 +178,9 @@ __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ 
     if (i >= N) return;
     const int c = cell_of[i];
     int pos = start[c] + rank[i];
-    if (ref && cnt[c] >= kBigCell) {
-        const int L = ref->L;
-        const int q1 = sub_bin(pts[(size_t)ref->axis0 * N + i], ref->lo0, ref->inv0, ref->nb1);
-        const int q2 = L > 1 ? sub_bin(pts[(size_t)ref->axis1 * N + i], ref->lo1, ref->inv1, ref->nb2) : 0;
+    if (subkey && cnt[c] >= kBigCell) {
         const size_t base = (size_t)bidx[c] * kSubBins;
-        pos += substart[base + q1 * ref->nb2 + q2] - substart[base];
+        pos += substart[base + subkey[i]] - substart[base];
     }
     sorted_idx[pos] = i;
     inv[i] = pos;
@@ -252,49 +250,263 @@ __global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restric
     }
 }
 
-// Picks the refinement axes among g..D-1 (largest variance first, lower index
-// on ties) and the sub-bin geometry.  One thread.
-__global__ void refine_setup_kernel(const DimStat* __restrict__ st, int g, int D, RefineInfo* __restrict__ info) {
+// Picks the projection terms among coordinates g..D-1 (the kMaxTerms largest
+// variances, lower index on ties), their centres, the sub-bin split and the
+// projection rounding margin.  One thread.
+//
+// Margin: with y_t = fl(x_t - m_t) = (x_t - m_t)(1 + d_t), |d_t| <= u, the
+// sequential fma chain over T terms satisfies
+//   |s - sum w_t (x_t - m_t)| <= (gamma_T (1 + u) + u) sum |w_t| |x_t - m_t|
+//                             <= (T + 2) u |x - m|     (|w| <= 1, Cauchy-Schwarz)
+// and |x - m|^2 <= sum_t max(hi_t - m_t, m_t - lo_t)^2 over the input.  A
+// non-finite bound (infinite input) is stored as +inf: one sub-bin then.
+__global__ void refine_terms_kernel(const DimStat* __restrict__ st, int g, int D, RefineInfo* __restrict__ info) {
     if (threadIdx.x != 0) return;
     const int nd = D - g;
-    int a0 = g, a1 = -1;
-    for (int d = g + 1; d < D; ++d)
-        if (st[d].var > st[a0].var) a0 = d;
-    for (int d = g; d < D; ++d)
-        if (d != a0 && (a1 < 0 || st[d].var > st[a1].var)) a1 = d;
-    RefineInfo r{};
-    r.L = nd >= 2 ? 2 : 1;
-    r.nb1 = r.L == 2 ? 32 : kSubBins;
-    r.nb2 = r.L == 2 ? 32 : 1;
-    r.axis0 = a0;
-    r.axis1 = r.L == 2 ? a1 : a0;
-    const float rng0 = st[a0].hi - st[a0].lo;
-    r.lo0 = st[a0].lo;
-    r.inv0 = (rng0 > 0.0f && rng0 < 3.0e38f) ? (float)r.nb1 / rng0 : 0.0f;
-    if (r.L == 2) {
-        const float rng1 = st[a1].hi - st[a1].lo;
-        r.lo1 = st[a1].lo;
-        r.inv1 = (rng1 > 0.0f && rng1 < 3.0e38f) ? (float)r.nb2 / rng1 : 0.0f;
+    const int T = nd < kMaxTerms ? nd : kMaxTerms;
+    unsigned long long taken0 = 0ull, taken1 = 0ull;
+    double R2 = 0.0;
+    for (int t = 0; t < kMaxTerms; ++t) {
+        info->coord[t] = 0;
+        info->mean[t] = 0.0f;
+        info->w0[t] = 0.0f;
+        info->w1[t] = 0.0f;
     }
-    if (!(r.lo0 > -3.0e38f && r.lo0 < 3.0e38f)) { r.lo0 = 0.0f; r.inv0 = 0.0f; }
-    if (!(r.lo1 > -3.0e38f && r.lo1 < 3.0e38f)) { r.lo1 = 0.0f; r.inv1 = 0.0f; }
-    *info = r;
+    for (int t = 0; t < T; ++t) {
+        int best = -1;
+        for (int d = g; d < D; ++d) {
+            const unsigned long long bit = 1ull << (d & 63);
+            if ((d < 64 ? taken0 : taken1) & bit) continue;
+            if (best < 0 || st[d].var > st[best].var) best = d;
+        }
+        if (best < 64) taken0 |= 1ull << best;
+        else taken1 |= 1ull << (best - 64);
+        const DimStat s = st[best];
+        info->coord[t] = best;
+        info->mean[t] = s.mean;
+        const double e = fmax((double)s.hi - (double)s.mean, (double)s.mean - (double)s.lo);
+        R2 += e * e;
+    }
+    const int L = T >= 2 ? 2 : 1;
+    info->L = L;
+    info->nb1 = L == 2 ? 32 : kSubBins;
+    info->nb2 = L == 2 ? 32 : 1;
+    info->terms = T;
+    info->lo0 = info->lo1 = info->inv0 = info->inv1 = 0.0f;
+    const double E = (T + 2) * 5.9604644775390625e-08 * sqrt(R2) * (1.0 + 9.765625e-04);
+    info->margin = E < 1.0e30 ? (float)(E * (1.0 + 9.5367431640625e-07)) : __builtin_huge_valf();
+    for (int k = 0; k < 7; ++k) info->pad[k] = 0;
 }
 
-// Sub-bin counting inside big cells; the arrival slot replaces the cell rank.
+// Pair p of the upper triangle (row-major over a <= b) of a T x T matrix.
+__device__ __forceinline__ void pair_of(int p, int T, int& a, int& b) {
+    a = 0;
+    while (p >= T - a) {
+        p -= T - a;
+        ++a;
+    }
+    b = a + p;
+}
+
+// Partial covariance sums of the projection terms: per block, the fp64 sum of
+// y_a * y_b (y = fl(x - mean), non-finite values as 0) for every pair a <= b.
+// A tile of 256 points is staged in LDS (row stride kMaxTerms + 1 so a wave's
+// reads of one point's terms hit distinct banks); threads split the pairs and,
+// with fewer than 256 pairs, the points of the tile.
+__global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts, int N,
+                                                  const RefineInfo* __restrict__ ri, double* __restrict__ part) {
+    constexpr int kStride = kMaxTerms + 1;
+    __shared__ float s_y[256 * kStride];
+    __shared__ double s_acc[256];
+    const int tid = threadIdx.x;
+    const int T = ri->terms;
+    const int P = T * (T + 1) / 2;
+    const int slices = P >= 256 ? 1 : 256 / P;
+    int pa[3] = {0, 0, 0}, pb[3] = {0, 0, 0};
+    int np = 0, slice = 0;
+    if (slices == 1) {
+        for (int p = tid; p < P; p += 256) {
+            pair_of(p, T, pa[np], pb[np]);
+            ++np;
+        }
+    } else if (tid < P * slices) {
+        pair_of(tid % P, T, pa[0], pb[0]);
+        slice = tid / P;
+        np = 1;
+    }
+    double acc[3] = {0.0, 0.0, 0.0};
+    for (long long base = (long long)blockIdx.x * 256; base < N; base += 256LL * gridDim.x) {
+        const long long i = base + tid;
+        for (int t = 0; t < T; ++t) {
+            float y = 0.0f;
+            if (i < N) {
+                y = pts[(size_t)ri->coord[t] * N + i] - ri->mean[t];
+                if (!(fabsf(y) <= 3.4e38f)) y = 0.0f;
+            }
+            s_y[tid * kStride + t] = y;
+        }
+        __syncthreads();
+        const int cnt = (int)min(256LL, (long long)N - base);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            if (k < np) {
+                double s = 0.0;
+                for (int j = slice; j < cnt; j += slices)
+                    s = fma((double)s_y[j * kStride + pa[k]], (double)s_y[j * kStride + pb[k]], s);
+                acc[k] += s;
+            }
+        }
+        __syncthreads();
+    }
+    double* out = part + (size_t)blockIdx.x * kMaxPairs;
+    if (slices == 1) {
+        for (int k = 0; k < np; ++k) out[tid + 256 * k] = acc[k];
+    } else {
+        s_acc[tid] = acc[0];
+        __syncthreads();
+        if (tid < P) {
+            double s = 0.0;
+            for (int sl = 0; sl < slices; ++sl) s += s_acc[sl * P + tid];
+            out[tid] = s;
+        }
+    }
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ double wave_max_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Reduces the covariance partials (fixed order), finds the top two principal
+// directions of the terms by subspace iteration with a final Rayleigh-Ritz
+// rotation (fp64, one wave, lane t = term t), and stores the weights scaled by
+// 1 - 2^-20 (so the fp32 weight vectors have norm < 1) with the sub-bin
+// geometry: each direction's bins span +-2.5 standard deviations of its
+// projections; points beyond clamp into the end bins.  Only quality depends on
+// these choices: the search's windows are exact for any weights of norm <= 1.
+__global__ __launch_bounds__(256) void refine_dirs_kernel(const double* __restrict__ part, int nblk, int N,
+                                                          RefineInfo* __restrict__ ri) {
+    __shared__ double s_C[kMaxTerms][kMaxTerms + 1];
+    const int tid = threadIdx.x;
+    const int T = ri->terms;
+    const int P = T * (T + 1) / 2;
+    for (int p = tid; p < P; p += 256) {
+        double s = 0.0;
+        for (int b = 0; b < nblk; ++b) s += part[(size_t)b * kMaxPairs + p];
+        int a, c;
+        pair_of(p, T, a, c);
+        s /= (double)N;
+        s_C[a][c] = s;
+        s_C[c][a] = s;
+    }
+    __syncthreads();
+    if (tid >= kWave) return;
+    const int t = tid;
+    const bool on = t < T;
+    auto matvec = [&](double v) {
+        double w = 0.0;
+        for (int j = 0; j < T; ++j) w = fma(s_C[on ? t : 0][j], __shfl(v, j), w);
+        return on ? w : 0.0;
+    };
+    // orthonormal (x0, x1) spanning what (x0, x1) span; degenerate inputs fall
+    // back to coordinate directions
+    auto orthonormalise = [&](double& x0, double& x1) {
+        double n0 = sqrt(wave_sum_f64(x0 * x0));
+        if (!(n0 > 1.0e-300 && n0 < 1.0e300)) {
+            x0 = (t == 0) ? 1.0 : 0.0;
+            n0 = 1.0;
+        }
+        x0 /= n0;
+        x1 -= wave_sum_f64(x1 * x0) * x0;
+        const double n1 = sqrt(wave_sum_f64(x1 * x1));
+        if (!(n1 > 1.0e-300 && n1 > 1.0e-14 * n0 && n1 < 1.0e300)) {
+            // e_k with k != argmax |x0| is never parallel to x0
+            const double m = fabs(x0);
+            const double mx = wave_max_f64(on ? m : -1.0);
+            const int kmax = __ffsll((long long)__ballot(on && m == mx)) - 1;
+            const int k = kmax == 0 ? 1 : 0;
+            x1 = (t == k) ? 1.0 : 0.0;
+            x1 -= wave_sum_f64(x1 * x0) * x0;
+            x1 /= sqrt(wave_sum_f64(x1 * x1));
+        } else {
+            x1 /= n1;
+        }
+    };
+    double u0, u1, l0, l1;
+    if (T == 1) {
+        u0 = (t == 0) ? 1.0 : 0.0;
+        u1 = 0.0;
+        l0 = s_C[0][0];
+        l1 = 0.0;
+    } else {
+        double v0 = on ? (t == 0 ? 1.0 : 0.0625 * (double)((t * 7) % 5 - 2)) : 0.0;
+        double v1 = on ? (t == 1 ? 1.0 : 0.0625 * (double)((t * 3) % 7 - 3)) : 0.0;
+        orthonormalise(v0, v1);
+        for (int it = 0; it < 48; ++it) {
+            v0 = matvec(v0);
+            v1 = matvec(v1);
+            orthonormalise(v0, v1);
+        }
+        const double c0 = matvec(v0), c1 = matvec(v1);
+        const double a = wave_sum_f64(v0 * c0), b = wave_sum_f64(v0 * c1), c = wave_sum_f64(v1 * c1);
+        const double th = 0.5 * atan2(2.0 * b, a - c);
+        const double cs = cos(th), sn = sin(th);
+        u0 = cs * v0 + sn * v1;
+        u1 = cs * v1 - sn * v0;
+        l0 = a * cs * cs + 2.0 * b * sn * cs + c * sn * sn;
+        l1 = a * sn * sn - 2.0 * b * sn * cs + c * cs * cs;
+    }
+    constexpr double kShrink = 1.0 - 9.5367431640625e-07;   // 1 - 2^-20
+    if (on) {
+        ri->w0[t] = (float)(u0 * kShrink);
+        ri->w1[t] = ri->L > 1 ? (float)(u1 * kShrink) : 0.0f;
+    }
+    if (t == 0) {
+        const bool exact = ri->margin < 1.0e30f;
+        float lo[2] = {0.0f, 0.0f}, inv[2] = {0.0f, 0.0f};
+        const double lam[2] = {l0, l1};
+        const int nb[2] = {ri->nb1, ri->nb2};
+        for (int k = 0; k < ri->L; ++k) {
+            const double sg = sqrt(fmax(lam[k], 0.0));
+            const double iv = (double)nb[k] / (5.0 * sg);
+            if (exact && sg > 0.0 && iv < 1.0e30) {
+                lo[k] = (float)(-2.5 * sg);
+                inv[k] = (float)iv;
+            }
+        }
+        ri->lo0 = lo[0];
+        ri->lo1 = lo[1];
+        ri->inv0 = inv[0];
+        ri->inv1 = inv[1];
+    }
+}
+
+// Sub-bin key and counting inside big cells; the arrival slot in the sub-bin
+// replaces the cell rank, and the key is kept for the reorder.
 __global__ __launch_bounds__(256) void sub_count_kernel(const float* __restrict__ pts, int N,
                                                         const int* __restrict__ cell_of,
                                                         const int* __restrict__ cnt,
                                                         const int* __restrict__ bidx,
                                                         const RefineInfo* __restrict__ ref,
-                                                        int* __restrict__ subcnt, int* __restrict__ rank) {
+                                                        int* __restrict__ subcnt, int* __restrict__ rank,
+                                                        int* __restrict__ subkey) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
     const int c = cell_of[i];
     if (cnt[c] < kBigCell) return;
-    const int q1 = sub_bin(pts[(size_t)ref->axis0 * N + i], ref->lo0, ref->inv0, ref->nb1);
-    const int q2 = ref->L > 1 ? sub_bin(pts[(size_t)ref->axis1 * N + i], ref->lo1, ref->inv1, ref->nb2) : 0;
-    rank[i] = atomicAdd(&subcnt[(size_t)bidx[c] * kSubBins + q1 * ref->nb2 + q2], 1);
+    float s0, s1;
+    refine_project(ref, [&](int d) { return pts[(size_t)d * N + i]; }, s0, s1);
+    const int q1 = sub_bin(s0, ref->lo0, ref->inv0, ref->nb1);
+    const int q2 = ref->L > 1 ? sub_bin(s1, ref->lo1, ref->inv1, ref->nb2) : 0;
+    const int key = q1 * ref->nb2 + q2;
+    subkey[i] = key;
+    rank[i] = atomicAdd(&subcnt[(size_t)bidx[c] * kSubBins + key], 1);
 }
 
 __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ pts, int N, int D, int ds,
@@ -378,6 +590,8 @@ RefineLayout refine_layout(int N, int D, long long cells) {
     L.substart = off; off = align256(off + (size_t)L.nsub * sizeof(int));
     const int np = scan_partials_count(L.nsub > cells + 1 ? L.nsub : (int)(cells + 1));
     L.scanpart = off; off = align256(off + (size_t)np * sizeof(int));
+    L.cov = off;      off = align256(off + (size_t)kCovBlocks * kMaxPairs * sizeof(double));
+    L.subkey = off;   off = align256(off + (size_t)N * sizeof(int));
     L.total = off;
     (void)D;
     return L;
@@ -413,13 +627,17 @@ int launch_refine(const float* pts, int N, int D, int g, long long cells, const 
     int* substart = reinterpret_cast<int*>(base + L.substart);
     int* scanpart = reinterpret_cast<int*>(base + L.scanpart);
     const DimStat* st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
-    hipLaunchKernelGGL(refine_setup_kernel, dim3(1), dim3(64), 0, s, st, g, D, info);
+    double* cov = reinterpret_cast<double*>(base + L.cov);
+    int* subkey = reinterpret_cast<int*>(base + L.subkey);
+    hipLaunchKernelGGL(refine_terms_kernel, dim3(1), dim3(64), 0, s, st, g, D, info);
+    hipLaunchKernelGGL(cov_kernel, dim3(kCovBlocks), dim3(256), 0, s, pts, N, info, cov);
+    hipLaunchKernelGGL(refine_dirs_kernel, dim3(1), dim3(256), 0, s, cov, kCovBlocks, N, info);
     int rc = launch_exclusive_scan(cnt, (int)cells + 1, bidx, scanpart, s, kBigCell);
     if (rc) return rc;
     rc = launch_fill_i32(subcnt, L.nsub, 0, s);
     if (rc) return rc;
     hipLaunchKernelGGL(sub_count_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, cell_of, cnt,
-                       bidx, info, subcnt, rank);
+                       bidx, info, subcnt, rank, subkey);
     rc = launch_exclusive_scan(subcnt, L.nsub, substart, scanpart, s);
     if (rc) return rc;
     return launch_result();
@@ -429,13 +647,13 @@ int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int
                    const int* cnt, const void* refine_ws, long long cells, int* sorted_idx, int* inv,
                    float* aos, const void* stats_ws, float* frows, float* fnorm, hipStream_t s) {
     if (N <= 0) return 0;
-    const RefineInfo* ref = nullptr;
+    const int* subkey = nullptr;
     const int* bidx = nullptr;
     const int* substart = nullptr;
     if (refine_ws) {
         const RefineLayout L = refine_layout(N, D, cells);
         const char* base = static_cast<const char*>(refine_ws);
-        ref = reinterpret_cast<const RefineInfo*>(base + L.info);
+        subkey = reinterpret_cast<const int*>(base + L.subkey);
         bidx = reinterpret_cast<const int*>(base + L.bidx);
         substart = reinterpret_cast<const int*>(base + L.substart);
     }
@@ -444,7 +662,7 @@ int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int
                                  : nullptr;
     if (!st) frows = nullptr;
     hipLaunchKernelGGL(reorder_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, D,
-                       aos_stride(D), cell_of, rank, start, cnt, ref, bidx, substart, sorted_idx, inv, aos,
+                       aos_stride(D), cell_of, rank, start, cnt, subkey, bidx, substart, sorted_idx, inv, aos,
                        st, frows, fnorm);
     return launch_result();
 }

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "frnn_internal.hpp"
+
 namespace frnn {
 
 constexpr int kWave = 64;
@@ -31,6 +33,25 @@ __device__ __forceinline__ int sub_bin(float x, float lo, float inv, int nb) {
     f = fmaxf(f, 0.0f);
     f = fminf(f, (float)(nb - 1));
     return (int)f;
+}
+
+// Projections of a point onto both refinement directions: for each, the
+// sequential fma chain over the terms of fl(x[coord[t]] - mean[t]) weighted by
+// w0[t] / w1[t] (w1 is zero with one direction), with coord(c) returning
+// coordinate c of the point.  The build (sub-bin keys) and the search (query
+// windows) both use it; each value is within RefineInfo::margin of the exact
+// projection.
+template <class Coord>
+__device__ __forceinline__ void refine_project(const RefineInfo* __restrict__ ri, Coord coord, float& s0,
+                                               float& s1) {
+    s0 = 0.0f;
+    s1 = 0.0f;
+    const int T = ri->terms;
+    for (int t = 0; t < T; ++t) {
+        const float y = coord(ri->coord[t]) - ri->mean[t];
+        s0 = fmaf(ri->w0[t], y, s0);
+        s1 = fmaf(ri->w1[t], y, s1);
+    }
 }
 
 // Total order on (d2, idx): non-negative fp32 bit patterns order like the

@@ -22,25 +22,33 @@ int scan_partials_count(int n);
 
 // ---- within-cell refinement -------------------------------------------------
 // Cells holding at least kBigCell points are ordered internally by a 2-D
-// sub-bin key on the two highest-variance non-grid axes (one axis when only
-// one non-grid axis exists), kSubBins sub-bins per big cell.  The search then
-// restricts each big cell to the sub-bins that intersect its queries' windows.
+// sub-bin key on the projections onto the two principal directions of the
+// non-grid coordinates (one direction when only one non-grid coordinate
+// exists), kSubBins sub-bins per big cell.  The search then restricts each big
+// cell to the sub-bins that intersect its queries' windows.
 constexpr int kBigCell = 256;
 constexpr int kSubBins = 1024;
 constexpr int kStatBlocks = 256;
+constexpr int kMaxTerms = FRNN_REFINE_TERMS;
+constexpr int kMaxPairs = kMaxTerms * (kMaxTerms + 1) / 2;   // covariance entries
+constexpr int kCovBlocks = 256;
 
 struct RefineInfo {
-    int L;              // refinement axes (0 = none)
-    int nb1, nb2;       // sub-bins per axis, nb1 * nb2 == kSubBins
-    int axis0, axis1;   // coordinates used
-    float lo0, lo1;     // bin origin per axis
-    float inv0, inv1;   // bins per unit per axis
+    int L;              // refinement directions (0 = none)
+    int nb1, nb2;       // sub-bins per direction, nb1 * nb2 == kSubBins
+    int terms;          // coordinates per projection
+    float lo0, lo1;     // bin origin per direction
+    float inv0, inv1;   // bins per unit per direction
+    float margin;       // bound on the projection rounding of any finite point
     int pad[7];
+    int coord[kMaxTerms];
+    float mean[kMaxTerms];
+    float w0[kMaxTerms], w1[kMaxTerms];
 };
 static_assert(sizeof(RefineInfo) == sizeof(frnn_refine_info_t), "RefineInfo mirrors frnn_refine_info_t");
 
 struct RefineLayout {
-    size_t info, bidx, subcnt, substart, scanpart, total;   // byte offsets
+    size_t info, bidx, subcnt, substart, scanpart, cov, subkey, total;   // byte offsets
     int max_big;        // upper bound on cells with >= kBigCell points
     int nsub;           // max_big * kSubBins + 1 scanned entries
 };

@@ -466,6 +466,9 @@ void search_kernel(SearchArgs a) {
         const float keep = 0.9999847412109375f;   // 1 - 2^-16
         const float eps = 4.76837158203125e-07f;  // 2^-21
         const int L = a.ref ? a.ref->L : 0;
+        // this lane's query projected onto the refinement directions
+        float pj0 = 0.0f, pj1 = 0.0f;
+        if (L > 0) refine_project(a.ref, [&](int d) { return qrow[d]; }, pj0, pj1);
 
         int seg = 0, seg_id = 0;
         while (seg < nq) {
@@ -487,23 +490,26 @@ void search_kernel(SearchArgs a) {
                 for (int d = 1; d < a.G; ++d) { s_rc[d] = Rt % a.res; Rt /= a.res; }
             }
             const float thr_seg = wave_max_f32(in_seg ? key_d2(s_thr[n]) : -__builtin_huge_valf());
-            // refinement windows: every candidate within the radius of a
-            // segment query has its axis coordinate inside [w_lo, w_hi]
+            // refinement windows: a candidate within the radius of a segment
+            // query q has |s(p) - s(q)| <= |p - q| + 2 margin on each direction
+            // (weights of norm < 1), so its projection lies in [lo - h, hi + h]
+            // over the segment's projections; h adds the fp32 distance slack
+            // (2^-15 relative) and the rounding of the window ends (2^-22 of
+            // |lo| + |hi|).  sub_bin is monotone, so the window is a sub-bin range.
             int qlo0 = 0, qhi0 = 0, qlo1 = 0, qhi1 = 0, nb2 = 1;
             if (L > 0) {
                 const RefineInfo* rf = a.ref;
                 nb2 = rf->nb2;
-                const float x0v = qrow[rf->axis0];
-                const float lo0 = wave_min_f32(in_seg ? x0v : __builtin_huge_valf());
-                const float hi0 = wave_max_f32(in_seg ? x0v : -__builtin_huge_valf());
-                const float h0 = a.radius * 1.000030517578125f + 2.384185791015625e-07f * (fabsf(lo0) + fabsf(hi0));
+                const float hw = a.radius * 1.000030517578125f + 2.0f * rf->margin;
+                const float lo0 = wave_min_f32(in_seg ? pj0 : __builtin_huge_valf());
+                const float hi0 = wave_max_f32(in_seg ? pj0 : -__builtin_huge_valf());
+                const float h0 = hw + 2.384185791015625e-07f * (fabsf(lo0) + fabsf(hi0));
                 qlo0 = sub_bin(lo0 - h0, rf->lo0, rf->inv0, rf->nb1);
                 qhi0 = sub_bin(hi0 + h0, rf->lo0, rf->inv0, rf->nb1);
                 if (L > 1) {
-                    const float x1v = qrow[rf->axis1];
-                    const float lo1 = wave_min_f32(in_seg ? x1v : __builtin_huge_valf());
-                    const float hi1 = wave_max_f32(in_seg ? x1v : -__builtin_huge_valf());
-                    const float h1 = a.radius * 1.000030517578125f + 2.384185791015625e-07f * (fabsf(lo1) + fabsf(hi1));
+                    const float lo1 = wave_min_f32(in_seg ? pj1 : __builtin_huge_valf());
+                    const float hi1 = wave_max_f32(in_seg ? pj1 : -__builtin_huge_valf());
+                    const float h1 = hw + 2.384185791015625e-07f * (fabsf(lo1) + fabsf(hi1));
                     qlo1 = sub_bin(lo1 - h1, rf->lo1, rf->inv1, rf->nb2);
                     qhi1 = sub_bin(hi1 + h1, rf->lo1, rf->inv1, rf->nb2);
                 }

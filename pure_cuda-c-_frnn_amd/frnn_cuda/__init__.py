@@ -50,6 +50,24 @@ class _Plan(ctypes.Structure):
                 "r2": self.r2, "cell_size": self.cell_size, "inv_cell": self.inv_cell}
 
 
+REFINE_TERMS = 32
+
+
+class RefineInfo(ctypes.Structure):
+    """frnn_refine_info_t: the descriptor at the start of a refinement workspace."""
+    _fields_ = [("axes", ctypes.c_int), ("bins0", ctypes.c_int), ("bins1", ctypes.c_int),
+                ("terms", ctypes.c_int), ("lo0", ctypes.c_float), ("lo1", ctypes.c_float),
+                ("inv0", ctypes.c_float), ("inv1", ctypes.c_float), ("margin", ctypes.c_float),
+                ("reserved", ctypes.c_int * 7), ("coord", ctypes.c_int * REFINE_TERMS),
+                ("mean", ctypes.c_float * REFINE_TERMS), ("w0", ctypes.c_float * REFINE_TERMS),
+                ("w1", ctypes.c_float * REFINE_TERMS)]
+
+    @classmethod
+    def from_workspace(cls, head):
+        """Decode from the first bytes of a refinement workspace (bytes or uint8 array)."""
+        return cls.from_buffer_copy(bytes(np.asarray(head, dtype=np.uint8)[:ctypes.sizeof(cls)]))
+
+
 _lib = None
 
 

@@ -116,10 +116,22 @@ def _sub_bins(x, lo, inv, nb):
     return f.astype(np.int64)
 
 
+def _project(X, ri):
+    """The refinement projections in fp32: s = fma(w[t], fl(x[coord[t]] - mean[t]), s)."""
+    s0 = np.zeros(len(X), np.float32)
+    s1 = np.zeros(len(X), np.float32)
+    for t in range(ri.terms):
+        y = (X[:, ri.coord[t]] - np.float32(ri.mean[t])).astype(np.float32)
+        s0 = E.fma32(np.float32(ri.w0[t]), y, s0)
+        s1 = E.fma32(np.float32(ri.w1[t]), y, s1)
+    return s0, s1
+
+
 @pytest.mark.parametrize("name,N", [("metric", 300_000), ("C3", 300_000)])
 def test_refinement_orders_big_cells(name, N):
-    """Within-cell refinement: axis choice, sub-bin order inside big cells, and the
-    usual permutation / cell-order / row-copy invariants of the reorder."""
+    """Within-cell refinement: the projection descriptor (terms, weights, margin,
+    bin geometry), the sub-bin order inside big cells, and the usual permutation /
+    cell-order / row-copy invariants of the reorder."""
     t = torch()
     w = W.config(name, N=N)
     plan = frnn_cuda._plan_struct(N, w.D, w.K, w.radius)
@@ -152,14 +164,53 @@ def test_refinement_orders_big_cells(name, N):
     assert L.frnn_launch_reorder(vp(d), N, w.D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
                                  vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), vp(fnorm), None) == 0
     t.cuda.synchronize()
-    head = ws[:64].cpu().numpy()
-    ints, flts = head.view(np.int32), head.view(np.float32)
-    axes, nb1, nb2, ax0, ax1 = (int(v) for v in ints[:5])
-    lo0, lo1, inv0, inv1 = (float(v) for v in flts[5:9])
-    var = w.X[:, g:].astype(np.float64).var(0)
-    order = np.argsort(-var, kind="stable")
-    assert axes == 2 and nb1 * nb2 == 1024
-    assert (ax0, ax1) == (g + order[0], g + order[1])
+    ri = frnn_cuda.RefineInfo.from_workspace(ws[:1024].cpu().numpy())
+    stats = sws[:16 * w.D].cpu().numpy().view(np.float32).reshape(w.D, 4)
+    mean, var, lo, hi = (stats[:, k] for k in range(4))
+    T = min(w.D - g, 32)
+    assert ri.axes == 2 and ri.bins0 * ri.bins1 == 1024 and ri.terms == T
+    # terms: the highest-variance non-grid coordinates, lower index on ties
+    order = g + np.argsort(-var[g:], kind="stable")
+    coord = np.array(ri.coord[:T])
+    assert np.array_equal(coord, order[:T])
+    assert np.array_equal(np.array(ri.mean[:T], np.float32), mean[coord])
+    W0 = np.array(ri.w0[:T], np.float64)
+    W1 = np.array(ri.w1[:T], np.float64)
+    assert np.linalg.norm(W0) < 1 and np.linalg.norm(W1) < 1
+    assert abs(np.linalg.norm(W0) - 1) < 1e-5 and abs(np.linalg.norm(W1) - 1) < 1e-5 and abs(W0 @ W1) < 1e-5
+    # the directions span the top-2 principal subspace of the terms
+    Y = (w.X[:, coord] - mean[coord]).astype(np.float64)
+    C = Y.T @ Y / N
+    ev, V = np.linalg.eigh(C)
+    top = V[:, ::-1][:, :2]
+    span = np.stack([W0, W1], 1)
+    assert np.linalg.norm(span.T @ top) ** 2 > 2 * 0.98, (ev[::-1][:3])
+    # bins span +-2.5 standard deviations of each projection
+    for wk, lok, invk, nbk in ((W0, ri.lo0, ri.inv0, ri.bins0), (W1, ri.lo1, ri.inv1, ri.bins1)):
+        sg = np.sqrt(wk @ C @ wk)
+        assert abs(lok + 2.5 * sg) <= 1e-3 * sg and abs(invk * 5 * sg / nbk - 1) <= 1e-3
+    # margin >= (T + 2) u |x - mean| over the input
+    R = np.sqrt(np.sum(np.maximum(hi[coord].astype(np.float64) - mean[coord], mean[coord] - lo[coord].astype(np.float64)) ** 2))
+    assert ri.margin >= (T + 2) * 2.0 ** -24 * R
+    assert ri.margin <= 1.01 * (T + 2) * 2.0 ** -24 * R
+    # the window bound: pairs within the radius project within r(1 + 2^-15) + 2 margin
+    s0, s1 = _project(w.X, ri)
+    rs = np.random.RandomState(5)
+    r = float(np.float32(w.radius))
+    r2 = np.float32(np.float32(w.radius) ** 2)
+    X64 = w.X.astype(np.float64)
+    n2 = np.sum(X64 ** 2, 1)
+    dmax = 0.0
+    for qb in np.array_split(rs.randint(0, N, 400), 8):
+        near = (n2[None, :] + n2[qb, None] - 2 * X64[qb] @ X64.T) <= (1.01 * r) ** 2
+        qq, pp = np.nonzero(near)
+        qq = qb[qq]
+        inside = E.dist2(w.X[qq], w.X[pp], 0) < r2
+        qq, pp = qq[inside], pp[inside]
+        for s in (s0, s1):
+            dmax = max(dmax, float(np.max(np.abs(s[pp].astype(np.float64) - s[qq]))))
+    assert 0 < dmax <= r * (1 + 2.0 ** -15) + 2 * ri.margin
+    # reorder invariants
     sidx, inv_p = sidx.cpu().numpy(), inv_p.cpu().numpy()
     cnt = cnt.cpu().numpy()[:cells]
     cells_of = O.bin_cells(w.X, g, res, np.float32(plan.inv_cell))
@@ -169,9 +220,8 @@ def test_refinement_orders_big_cells(name, N):
     assert np.all(np.diff(cs) >= 0)
     rows = aos.cpu().numpy().reshape(N, ds)
     assert np.array_equal(rows[:, :w.D], w.X[sidx])
-    key = _sub_bins(w.X[sidx, ax0], lo0, inv0, nb1) * nb2 + _sub_bins(w.X[sidx, ax1], lo1, inv1, nb2)
+    key = _sub_bins(s0[sidx], ri.lo0, ri.inv0, ri.bins0) * ri.bins1 + _sub_bins(s1[sidx], ri.lo1, ri.inv1, ri.bins1)
     # filter rows: fl(x - mean) and their sequential-fma squared norms
-    mean = sws[:16 * w.D].cpu().numpy().view(np.float32).reshape(w.D, 4)[:, 0]
     fr = frows.cpu().numpy().reshape(N, ds)
     assert np.array_equal(fr[:, :w.D], (w.X[sidx] - mean[None, :]).astype(np.float32))
     assert np.all(fr[:, w.D:] == 0)
@@ -181,6 +231,8 @@ def test_refinement_orders_big_cells(name, N):
     same_cell = np.concatenate([[False], cs[1:] == cs[:-1]])
     step = np.concatenate([[0], np.diff(key)])
     assert np.all(step[same_cell & big] >= 0)
+    # the keys are not all equal: the refinement splits the big cells
+    assert len(np.unique(key[big])) > 256
 
 
 def test_point_stats():
