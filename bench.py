@@ -9,10 +9,14 @@ in HBM and the outputs left in HBM -- the timing the reference's harness uses
 (Tests/scripts/benchmark_vs_libfrnn.py:146-169).  Prints ONE JSON line on stdout:
 
   value            mean ms per step over exactly K steps (sync before and after)
-  roofline         dominant kernel (the neighbour search): algorithmic fp32 flops
-                   (2*D per shell candidate pair) / its mean HIP-event duration,
-                   against the fp32 MFMA peak; traffic from the committed
-                   rocprofv3 PMC summary when present
+  roofline         dominant kernel (the neighbour search): fp32 flops of its
+                   distance filter -- 2*D per (query, candidate) pair streamed
+                   through the filter, counted live by the kernel -- / its mean
+                   HIP-event duration, against the fp32 MFMA peak; traffic (HBM
+                   bytes per launch) from the committed rocprofv3 PMC summary when
+                   present.  hbm_view: the search's algorithmic bytes
+                   8DN + 4(C+1) + 4N + 8KN (read rows, cell offsets, index map;
+                   write K keys per query) over the same duration vs 8 TB/s.
   build_hbm        grid-build kernels: algorithmic bytes / event time vs 8 TB/s
   cpu_baseline     the C++/OpenMP restatement (oracle/) on a bounded query sample,
                    timed on this host, extrapolated to all N queries; the same
@@ -49,9 +53,13 @@ def build_bytes(N, D, ds, g, C, refine):
         "reorder": 20 * N + 4 * D * N + 8 * ds * N + 4 * N,
     }
     if refine:
-        # big-cell flags scan + sub-bin count (cell, count, 2 axis coords, rank) + sub-bin scan
+        # big-cell flags scan + covariance pass over the T projection terms + sub-bin
+        # count (cell, count, big-cell index, T terms; writes rank and key) + sub-bin
+        # fill and scan; the reorder also reads the keys
+        T = min(D - g, 32)
         nsub = (N // 256) * 1024 + 1
-        b["refine"] = 8 * (C + 1) + 20 * N + 12 * nsub
+        b["refine"] = 8 * (C + 1) + 4 * T * N + (20 + 4 * T) * N + 12 * nsub
+        b["reorder"] += 4 * N
     return b
 
 
@@ -147,18 +155,24 @@ def main():
     gi = idx.reshape(w.K, w.N).T
     gd = dist.reshape(w.K, w.N).T
 
-    # dominant kernel roofline: fp32 MFMA
-    pairs = ctr["shell_candidates"]
+    # dominant kernel roofline: fp32 MFMA over the pairs the distance filter evaluates
+    pairs = ctr["streamed_pairs"]
     flops = 2.0 * w.D * pairs
     search_s = stages["search"] / 1e3
     achieved = flops / search_s / 1e12
     traffic, traffic_src = traffic_from_profiles(args.config)
+    C = plan["cells"] if plan["path"] != "bruteforce" else 0
+    alg_bytes = 8 * w.D * w.N + 4 * (C + 1) + 4 * w.N + 8 * w.K * w.N
+    alg_gbs = alg_bytes / search_s / 1e9
     roofline = {"kernel": "search_kernel (neighbour search)", "bound": "mfma",
                 "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4), "traffic": traffic,
-                "flops_per_launch": flops, "shell_candidate_pairs": pairs,
+                "flops_per_launch": flops, "filtered_pairs": pairs,
+                "shell_candidate_pairs": ctr["shell_candidates"],
                 "mean_kernel_ms": round(stages["search"], 4),
-                "traffic_source": traffic_src}
+                "traffic_source": traffic_src,
+                "hbm_view": {"algorithmic_bytes": alg_bytes, "GBps": round(alg_gbs, 1),
+                             "frac": round(alg_gbs / HBM_PEAK_GBS, 5)}}
 
     if plan["path"] != "bruteforce":
         bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"], plan["cells"],

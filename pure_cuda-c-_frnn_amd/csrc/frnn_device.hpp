@@ -63,6 +63,60 @@ __device__ __forceinline__ float key_d2(unsigned long long key) {
     return __uint_as_float((unsigned int)(key >> 32));
 }
 
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int mask) {
+    const unsigned int lo = (unsigned int)__shfl_xor((int)(unsigned int)v, mask);
+    const unsigned int hi = (unsigned int)__shfl_xor((int)(unsigned int)(v >> 32), mask);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int src) {
+    const unsigned int lo = (unsigned int)__shfl((int)(unsigned int)v, src);
+    const unsigned int hi = (unsigned int)__shfl((int)(unsigned int)(v >> 32), src);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// Ascending bitonic sort of the 64*E keys held across one wave, x[e] being
+// element e*64 + lane.  Steps with a partner distance below 64 exchange through
+// lane shuffles; longer distances pair registers of the same lane.  No LDS and
+// no barriers.
+template <int E>
+__device__ __forceinline__ void wave_sort_u64(unsigned long long (&x)[E]) {
+    static_assert(E == 1 || E == 2 || E == 4 || E == 8, "power-of-two register count");
+    constexpr int kLogP = 6 + (E == 1 ? 0 : E == 2 ? 1 : E == 4 ? 2 : 3);
+    const int lane = threadIdx.x & (kWave - 1);
+    // affine loops over log2 distances so that both unroll fully and x[] stays in registers
+#pragma unroll
+    for (int lk = 1; lk <= kLogP; ++lk) {
+        const int k = 1 << lk;
+#pragma unroll
+        for (int lj = lk - 1; lj >= 0; --lj) {
+            const int j = 1 << lj;
+            if (j >= kWave) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int ep = e ^ (j / kWave);
+                    if (ep > e) {
+                        const bool up = ((e * kWave) & k) == 0;
+                        const unsigned long long p = x[e], q = x[ep];
+                        const bool sw = (p > q) == up;
+                        x[e] = sw ? q : p;
+                        x[ep] = sw ? p : q;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const unsigned long long y = shfl_xor_u64(x[e], j);
+                    const bool up = (((e * kWave) | lane) & k) == 0;
+                    const bool keep_min = ((lane & j) == 0) == up;
+                    const bool lt = x[e] < y;
+                    x[e] = (lt == keep_min) ? x[e] : y;
+                }
+            }
+        }
+    }
+}
+
 __device__ __forceinline__ int wave_min_i32(int v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));

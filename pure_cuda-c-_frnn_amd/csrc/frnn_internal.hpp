@@ -14,9 +14,10 @@ __host__ __device__ inline int aos_stride(int D) {
     return D <= 4 ? 4 : D <= 8 ? 8 : D <= 12 ? 12 : D <= 16 ? 16 : D <= 32 ? 32 : D <= 64 ? 64 : 128;
 }
 
-// Per-query candidate list entries: K kept after a compaction plus room for a
-// full 64-entry recheck batch and K more arrivals between compactions.
-inline int list_capacity(int K) { return 2 * K + 64; }
+// Per-query candidate list entries: K kept after a compaction, room for a full
+// 64-entry recheck batch and at least 64 more arrivals between compactions.
+// At most 256, the largest register sort of the search kernel.
+inline int list_capacity(int K) { return K + 128; }
 
 int scan_partials_count(int n);
 

@@ -24,9 +24,9 @@
 //     queued in LDS and re-evaluated 64 at a time with the reference's exact fp32
 //     distance order; accepted (d2, idx) keys go to a per-query candidate list;
 //   * when a list nears capacity the wave sorts it cooperatively (bitonic in
-//     LDS), keeps the K smallest and tightens the query's threshold to the K-th
-//     key; at the end every list is sorted and its first K keys (plus padding)
-//     are the result for that sorted position.
+//     registers, up to 4 keys per lane), keeps the K smallest and tightens the
+//     query's threshold to the K-th key; at the end every list is sorted and its
+//     first K keys (plus padding) are the result for that sorted position.
 //
 // Exactness: a pair is returned iff its exact fp32 distance in the reference
 // order is < r2 and it is among the K smallest (d2, idx) keys.  The MFMA value
@@ -42,8 +42,20 @@ namespace frnn {
 
 constexpr int kQB = 32;                      // queries per wave
 constexpr int kBatch = 64;                   // exact re-evaluations per batch
-constexpr int kQueueCap = kBatch + 4 * kWave;  // leftover batch + one register group of hits
-constexpr int kSortCap = 512;                // >= next_pow2(list_capacity(128))
+constexpr int kQueueCap = kBatch + 16 * kWave;  // leftover batch + one tile's hits
+static_assert(FRNN_MAX_K + 128 <= 4 * kWave, "a candidate list fits the largest register sort");
+
+template <int V>
+struct IntC { static constexpr int value = V; };
+
+// Workgroups are one wave, so lanes only need their LDS accesses ordered: an
+// LDS-only fence around the barrier leaves outstanding global loads (the
+// prefetched tile) in flight, where __syncthreads() would wait for them.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 constexpr int kRing = 128;                   // pending candidate runs (<= 31 + 64 in use)
 constexpr int kMaxG = 9;
 
@@ -59,10 +71,11 @@ struct SearchArgs {
     unsigned long long* lists;   // [N][cap] candidate keys
     unsigned long long* counters;
     int N, K, cap, G, res;
+    int room;                    // usable list entries: min(cap, largest register sort)
     float r2, cell, inv_cell, radius;
     float norm_scale;            // 1 - c_norm
     float thr_rel, thr_abs;      // filter threshold margin
-    int nchunks, chunks_per_xcd;
+    int nchunks;
 };
 
 __device__ __forceinline__ float filter_threshold(float thr, const SearchArgs& a) {
@@ -142,7 +155,6 @@ void search_kernel(SearchArgs a) {
     __shared__ unsigned long long s_thr[kQB];
     __shared__ int s_qn[kQueueCap];
     __shared__ int s_qpos[kQueueCap];
-    __shared__ unsigned long long s_sort[kSortCap];
     __shared__ int s_qsize;
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points,
     // virtual stream positions [vbeg, vend), cell x and row-segment id
@@ -155,10 +167,11 @@ void search_kernel(SearchArgs a) {
     const int lane = threadIdx.x;
     const int n = lane & 31;
     const int h = lane >> 5;
-    // The dispatcher places workgroup b on XCD b % 8; give each XCD a
-    // contiguous range of chunks so neighbouring queries share its L2.
-    const int b = blockIdx.x;
-    const int chunk = (b & 7) * a.chunks_per_xcd + (b >> 3);
+    // Workgroup b runs on XCD b % 8, so consecutive chunks of the cell order
+    // spread over all XCDs.  Work per chunk follows the point density, and a
+    // contiguous range per XCD left the XCDs holding dense regions finishing
+    // up to 2x later than the rest; interleaving keeps them balanced.
+    const int chunk = blockIdx.x;
     if (chunk >= a.nchunks) return;
     const int q0 = chunk * kQB;
     const int nq = min(kQB, a.N - q0);
@@ -181,7 +194,7 @@ void search_kernel(SearchArgs a) {
         s_thr[lane] = make_key(a.r2, 0);
     }
     if (lane == 0) s_qsize = 0;
-    __syncthreads();
+    lds_sync();
     // B operand: this lane's half of query n's centred row, scaled by -2, plus
     // the norm column.  Rows of a chunk are the sorted points q0..q0+31.
     float bop[HD + 1];
@@ -208,53 +221,69 @@ void search_kernel(SearchArgs a) {
 
     long long c_shell = 0, c_hit = 0, c_acc = 0, c_ovf = 0, c_stream = 0;
 
-    auto select_topk = [&](int qn, bool final_pass) {
-        const int c = s_cnt[qn];
-        int P = kWave;
-        while (P < c) P <<= 1;
+    // Sort query qn's candidate list in registers (wave_sort_u64 over the
+    // smallest power-of-two multiple of 64 holding it, ~0 filling the rest).
+    // Compaction keeps the K smallest keys and tightens the query's threshold
+    // to the K-th; the final pass writes the K smallest (padded with (r2, -1)).
+    auto select_sized = [&](auto e_const, int qn, int c, bool final_pass) __attribute__((always_inline)) {
+        constexpr int E = decltype(e_const)::value;
         unsigned long long* L = lists + (size_t)qn * a.cap;
-        for (int i = lane; i < P; i += kWave) s_sort[i] = (i < c) ? L[i] : ~0ull;
-        __syncthreads();
-        for (int k = 2; k <= P; k <<= 1) {
-            for (int j = k >> 1; j > 0; j >>= 1) {
-                for (int i = lane; i < P; i += kWave) {
-                    const int ixj = i ^ j;
-                    if (ixj > i) {
-                        const unsigned long long x = s_sort[i];
-                        const unsigned long long y = s_sort[ixj];
-                        const bool up = (i & k) == 0;
-                        if ((x > y) == up) {
-                            s_sort[i] = y;
-                            s_sort[ixj] = x;
-                        }
-                    }
-                }
-                __syncthreads();
-            }
+        // the list entries were stored by other lanes of this wave
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        unsigned long long x[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = e * kWave + lane;
+            x[e] = (i < c) ? L[i] : ~0ull;
         }
+        wave_sort_u64<E>(x);
         if (final_pass) {
             const unsigned long long pad = make_key(a.r2, -1);
-            for (int k = lane; k < a.K; k += kWave) L[k] = (k < c) ? s_sort[k] : pad;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int i = e * kWave + lane;
+                if (i < a.K) L[i] = (i < c) ? x[e] : pad;
+            }
+            // K may exceed the sorted span (few candidates, K > 64)
+            for (int i = E * kWave + lane; i < a.K; i += kWave) L[i] = pad;
         } else {
             const int keep = min(c, a.K);
-            for (int k = lane; k < keep; k += kWave) L[k] = s_sort[k];
-            if (lane == 0) {
-                s_cnt[qn] = keep;
-                if (c >= a.K) s_thr[qn] = s_sort[a.K - 1];
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int i = e * kWave + lane;
+                if (i < keep) L[i] = x[e];
             }
+            if (c >= a.K) {
+                const int ek = (a.K - 1) / kWave;
+                unsigned long long kth = x[0];
+#pragma unroll
+                for (int e = 1; e < E; ++e)
+                    if (e == ek) kth = x[e];
+                kth = shfl_u64(kth, (a.K - 1) & (kWave - 1));
+                if (lane == 0) s_thr[qn] = kth;
+            }
+            if (lane == 0) s_cnt[qn] = keep;
         }
-        __syncthreads();
+        lds_sync();
+    };
+    auto select_topk = [&](int qn, bool final_pass) __attribute__((always_inline)) {
+        const int c = s_cnt[qn];
+        if (c <= kWave) select_sized(IntC<1>{}, qn, c, final_pass);
+        else if (c <= 2 * kWave) select_sized(IntC<2>{}, qn, c, final_pass);
+        else select_sized(IntC<4>{}, qn, c, final_pass);
     };
 
-    auto process_batch = [&](int base, int count) {
-        // make room for a full batch in every list
-        const bool need = (lane < kQB) && (s_cnt[lane] > a.cap - kBatch);
+    // Exact re-evaluation of queue entries [base, base + count).  First every
+    // list that could overflow during the batch is compacted; with final_pass
+    // every list of the chunk gets its final selection instead.
+    auto process_batch = [&](int base, int count, bool final_pass) __attribute__((always_inline)) {
+        const bool need = (lane < kQB) && (final_pass ? lane < nq : s_cnt[lane] > a.room - kBatch);
         unsigned long long m = __ballot(need);
         if (m) {
             while (m) {
                 const int qn = __ffsll((long long)m) - 1;
                 m &= m - 1;
-                select_topk(qn, false);
+                select_topk(qn, final_pass);
             }
             if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
         }
@@ -268,14 +297,14 @@ void search_kernel(SearchArgs a) {
                 const int slot = atomicAdd(&s_cnt[qn], 1);
                 // compaction above leaves >= kBatch free slots; the guard only
                 // keeps a logic error from writing past the list
-                if (slot < a.cap) lists[(size_t)qn * a.cap + slot] = key;
+                if (slot < a.room) lists[(size_t)qn * a.cap + slot] = key;
                 else ++c_ovf;
                 ++c_acc;
             }
         }
-        __syncthreads();
+        lds_sync();
         if (lane == 0) s_qsize = base;
-        __syncthreads();
+        lds_sync();
     };
 
     // ---- candidate stream -------------------------------------------------
@@ -291,7 +320,7 @@ void search_kernel(SearchArgs a) {
         float op[HD + 1];
         int pos, x, seg, count;
     };
-    auto gather = [&](int v0, int count, Tile& t) {
+    auto gather = [&](int v0, int count, Tile& t) __attribute__((always_inline)) {
         const int v = v0 + n;
         const bool mvalid = n < count;
         t.count = count;
@@ -317,7 +346,7 @@ void search_kernel(SearchArgs a) {
     };
 
     // MFMA filter of one gathered tile: the 32 x 32 accumulator of filter values.
-    auto mfma_tile = [&](const Tile& t) {
+    auto mfma_tile = [&](const Tile& t) __attribute__((always_inline)) {
         floatx16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
@@ -329,7 +358,7 @@ void search_kernel(SearchArgs a) {
 
     // Queue the tile's hits (filter value below the query's threshold, candidate
     // inside the query's shell) for exact re-evaluation.
-    auto hits_tile = [&](const Tile& t, const floatx16& acc) {
+    auto hits_tile = [&](const Tile& t, const floatx16& acc) __attribute__((always_inline)) {
         if (h == 0) {
             t_pos[n] = t.pos;
             t_x[n] = t.x;
@@ -349,12 +378,12 @@ void search_kernel(SearchArgs a) {
             }
         }
         if (__ballot(gh[0] || gh[1] || gh[2] || gh[3]) == 0) return;
-        __syncthreads();
-        // four groups of four registers: at most 4 hits per lane per group, so
-        // the queue never exceeds 63 + 256 entries
+        lds_sync();
+        // All hits of the tile are queued first (at most 16 per lane, so the
+        // queue never exceeds 63 + 1024 entries); the exact batches run after,
+        // when the accumulator registers are no longer live.
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-            if (__ballot(gh[g4]) == 0) continue;
             if (gh[g4]) {
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
@@ -379,19 +408,19 @@ void search_kernel(SearchArgs a) {
                     }
                 }
             }
-            __syncthreads();
-            int qs = min(s_qsize, kQueueCap);
-            while (qs >= kBatch) {
-                process_batch(qs - kBatch, kBatch);
-                qs -= kBatch;
-            }
+        }
+        lds_sync();
+        int qs = min(s_qsize, kQueueCap);
+        while (qs >= kBatch) {
+            process_batch(qs - kBatch, kBatch, false);
+            qs -= kBatch;
         }
     };
 
     // Stream the available candidates: each tile's MFMA chain is issued first,
     // then (PREFETCH) the next tile's rows are gathered, so those loads are in
     // flight while the MFMAs run and the current tile's hits are handled.
-    auto consume = [&](bool final_pass) {
+    auto consume = [&](bool final_pass) __attribute__((always_inline)) {
         int avail = v_total - v_done;
         if (!(avail >= 32 || (final_pass && avail > 0))) return;
         Tile cur;
@@ -419,7 +448,7 @@ void search_kernel(SearchArgs a) {
     };
 
     // Append at most one run per lane (in lane order) to the ring.
-    auto append_runs = [&](int start, int len, int x, int seg) {
+    auto append_runs = [&](int start, int len, int x, int seg) __attribute__((always_inline)) {
         const bool has = len > 0;
         const unsigned long long mask = __ballot(has);
         if (mask == 0) return;
@@ -441,14 +470,14 @@ void search_kernel(SearchArgs a) {
         }
         ring_head += __popcll(mask);
         v_total += total;
-        __syncthreads();
+        lds_sync();
     };
 
     if constexpr (BF) {
         if (qvalid && h == 0) c_shell += a.N;
         my_seg = qvalid ? 0 : -1;
         append_runs(0, lane == 0 ? a.N : 0, 0, 0);
-        consume(false);
+        consume(true);
     } else {
         const float* qrow = s_q + n * DS;
         x_n = bin_coord(qrow[0], a.inv_cell, a.res);
@@ -470,74 +499,88 @@ void search_kernel(SearchArgs a) {
         float pj0 = 0.0f, pj1 = 0.0f;
         if (L > 0) refine_project(a.ref, [&](int d) { return qrow[d]; }, pj0, pj1);
 
-        int seg = 0, seg_id = 0;
-        while (seg < nq) {
-            const int R = __shfl(row_n, seg);
-            const bool in_seg = (row_n == R);
-            if (in_seg) my_seg = seg_id;
-            const int xlo = wave_min_i32(in_seg ? x_n : 0x7fffffff);
-            const int xhi = wave_max_i32(in_seg ? x_n : -1);
-            const int seg_end = __popcll(__ballot(row_n <= R) & 0xffffffffull);
-            // segment bounding box on the gridded axes and the largest threshold
-            for (int d = 0; d < a.G; ++d) {
-                const float qd = qrow[d];
-                const float lo = wave_min_f32(in_seg ? qd : __builtin_huge_valf());
-                const float hi = wave_max_f32(in_seg ? qd : -__builtin_huge_valf());
-                if (lane == 0) { s_blo[d] = lo; s_bhi[d] = hi; }
-            }
-            if (lane == 0) {
-                int Rt = R;
-                for (int d = 1; d < a.G; ++d) { s_rc[d] = Rt % a.res; Rt /= a.res; }
-            }
-            const float thr_seg = wave_max_f32(in_seg ? key_d2(s_thr[n]) : -__builtin_huge_valf());
-            // refinement windows: a candidate within the radius of a segment
-            // query q has |s(p) - s(q)| <= |p - q| + 2 margin on each direction
-            // (weights of norm < 1), so its projection lies in [lo - h, hi + h]
-            // over the segment's projections; h adds the fp32 distance slack
-            // (2^-15 relative) and the rounding of the window ends (2^-22 of
-            // |lo| + |hi|).  sub_bin is monotone, so the window is a sub-bin range.
-            int qlo0 = 0, qhi0 = 0, qlo1 = 0, qhi1 = 0, nb2 = 1;
-            if (L > 0) {
-                const RefineInfo* rf = a.ref;
-                nb2 = rf->nb2;
-                const float hw = a.radius * 1.000030517578125f + 2.0f * rf->margin;
-                const float lo0 = wave_min_f32(in_seg ? pj0 : __builtin_huge_valf());
-                const float hi0 = wave_max_f32(in_seg ? pj0 : -__builtin_huge_valf());
-                const float h0 = hw + 2.384185791015625e-07f * (fabsf(lo0) + fabsf(hi0));
-                qlo0 = sub_bin(lo0 - h0, rf->lo0, rf->inv0, rf->nb1);
-                qhi0 = sub_bin(hi0 + h0, rf->lo0, rf->inv0, rf->nb1);
-                if (L > 1) {
-                    const float lo1 = wave_min_f32(in_seg ? pj1 : __builtin_huge_valf());
-                    const float hi1 = wave_max_f32(in_seg ? pj1 : -__builtin_huge_valf());
-                    const float h1 = hw + 2.384185791015625e-07f * (fabsf(lo1) + fabsf(hi1));
-                    qlo1 = sub_bin(lo1 - h1, rf->lo1, rf->inv1, rf->nb2);
-                    qhi1 = sub_bin(hi1 + h1, rf->lo1, rf->inv1, rf->nb2);
+        // One loop walks the segments (runs of queries sharing a row) and, per
+        // segment, batches of 64 traversal items; every iteration appends at
+        // most one run per lane and streams what is available, so the tile
+        // loop below is inlined once.
+        int seg = 0, seg_id = -1;
+        int ib = 0, NI = 0;
+        int xa = 0, nx = 1, nq1 = 1, qlo0 = 0, qlo1 = 0, qhi1 = 0, nb2 = 1;
+        float thr_seg = 0.0f;
+        bool last = false;
+        while (!last) {
+            if (ib >= NI && seg < nq) {
+                ++seg_id;
+                const int R = __shfl(row_n, seg);
+                const bool in_seg = (row_n == R);
+                if (in_seg) my_seg = seg_id;
+                const int xlo = wave_min_i32(in_seg ? x_n : 0x7fffffff);
+                const int xhi = wave_max_i32(in_seg ? x_n : -1);
+                seg = __popcll(__ballot(row_n <= R) & 0xffffffffull);
+                // segment bounding box on the gridded axes and the largest threshold
+                for (int d = 0; d < a.G; ++d) {
+                    const float qd = qrow[d];
+                    const float lo = wave_min_f32(in_seg ? qd : __builtin_huge_valf());
+                    const float hi = wave_max_f32(in_seg ? qd : -__builtin_huge_valf());
+                    if (lane == 0) { s_blo[d] = lo; s_bhi[d] = hi; }
                 }
-            }
-            __syncthreads();
-
-            if (a.counters && in_seg && h == 0) {
-                for (int t = 0; t < nrows; ++t) {
-                    int tt = t, Rn = 0, mul = 1;
-                    bool ok = true;
-                    for (int d = 1; d < a.G; ++d) {
-                        const int cc = s_rc[d] + (tt % 3) - 1;
-                        tt /= 3;
-                        ok = ok && cc >= 0 && cc < a.res;
-                        Rn += cc * mul;
-                        mul *= a.res;
+                if (lane == 0) {
+                    int Rt = R;
+                    for (int d = 1; d < a.G; ++d) { s_rc[d] = Rt % a.res; Rt /= a.res; }
+                }
+                thr_seg = wave_max_f32(in_seg ? key_d2(s_thr[n]) : -__builtin_huge_valf());
+                // refinement windows: a candidate within the radius of a segment
+                // query q has |s(p) - s(q)| <= |p - q| + 2 margin on each direction
+                // (weights of norm < 1), so its projection lies in [lo - h, hi + h]
+                // over the segment's projections; h adds the fp32 distance slack
+                // (2^-15 relative) and the rounding of the window ends (2^-22 of
+                // |lo| + |hi|).  sub_bin is monotone, so the window is a sub-bin range.
+                int qhi0 = 0;
+                qlo0 = qlo1 = qhi1 = 0;
+                nb2 = 1;
+                if (L > 0) {
+                    const RefineInfo* rf = a.ref;
+                    nb2 = rf->nb2;
+                    const float hw = a.radius * 1.000030517578125f + 2.0f * rf->margin;
+                    const float lo0 = wave_min_f32(in_seg ? pj0 : __builtin_huge_valf());
+                    const float hi0 = wave_max_f32(in_seg ? pj0 : -__builtin_huge_valf());
+                    const float h0 = hw + 2.384185791015625e-07f * (fabsf(lo0) + fabsf(hi0));
+                    qlo0 = sub_bin(lo0 - h0, rf->lo0, rf->inv0, rf->nb1);
+                    qhi0 = sub_bin(hi0 + h0, rf->lo0, rf->inv0, rf->nb1);
+                    if (L > 1) {
+                        const float lo1 = wave_min_f32(in_seg ? pj1 : __builtin_huge_valf());
+                        const float hi1 = wave_max_f32(in_seg ? pj1 : -__builtin_huge_valf());
+                        const float h1 = hw + 2.384185791015625e-07f * (fabsf(lo1) + fabsf(hi1));
+                        qlo1 = sub_bin(lo1 - h1, rf->lo1, rf->inv1, rf->nb2);
+                        qhi1 = sub_bin(hi1 + h1, rf->lo1, rf->inv1, rf->nb2);
                     }
-                    if (!ok) continue;
-                    const int base = Rn * a.res;
-                    c_shell += a.start[base + min(x_n + 1, a.res - 1) + 1] - a.start[base + max(x_n - 1, 0)];
                 }
-            }
+                lds_sync();
 
-            const int xa = max(xlo - 1, 0);
-            const int nx = min(xhi + 1, a.res - 1) - xa + 1;
-            const int nq1 = L > 0 ? max(qhi0 - qlo0 + 1, 0) : 1;
-            const int NI = nx * nrows * nq1;
-            for (int ib = 0; ib < NI; ib += kWave) {
+                if (a.counters && in_seg && h == 0) {
+                    for (int t = 0; t < nrows; ++t) {
+                        int tt = t, Rn = 0, mul = 1;
+                        bool ok = true;
+                        for (int d = 1; d < a.G; ++d) {
+                            const int cc = s_rc[d] + (tt % 3) - 1;
+                            tt /= 3;
+                            ok = ok && cc >= 0 && cc < a.res;
+                            Rn += cc * mul;
+                            mul *= a.res;
+                        }
+                        if (!ok) continue;
+                        const int base = Rn * a.res;
+                        c_shell += a.start[base + min(x_n + 1, a.res - 1) + 1] - a.start[base + max(x_n - 1, 0)];
+                    }
+                }
+
+                xa = max(xlo - 1, 0);
+                nx = min(xhi + 1, a.res - 1) - xa + 1;
+                nq1 = L > 0 ? max(qhi0 - qlo0 + 1, 0) : 1;
+                NI = nx * nrows * nq1;
+                ib = 0;
+            }
+            if (ib < NI) {
                 const int item = ib + lane;
                 int rs = 0, rl = 0, rxv = 0;
                 if (item < NI) {
@@ -595,20 +638,21 @@ void search_kernel(SearchArgs a) {
                     }
                 }
                 append_runs(rs, rl, rxv, seg_id);
-                consume(false);
+                ib += kWave;
             }
-            seg = seg_end;
-            ++seg_id;
+            last = ib >= NI && seg >= nq;
+            consume(last);
         }
     }
-    consume(true);
 
-    __syncthreads();
+    lds_sync();
     {
+        // the last partial batch, then the final selection of every list
+        // (one call site for both keeps a single inlined copy of the sorts)
         const int qs = min(s_qsize, kQueueCap);
-        if (qs > 0) process_batch(0, qs);
+#pragma nounroll
+        for (int pass = 0; pass < 2; ++pass) process_batch(0, pass == 0 ? qs : 0, pass == 1);
     }
-    for (int qn = 0; qn < nq; ++qn) select_topk(qn, true);
 
     if (a.counters) {
         const long long s0 = wave_sum_i64(c_shell);
@@ -628,7 +672,7 @@ void search_kernel(SearchArgs a) {
 
 template <int DS, bool REV, bool BF>
 static void launch_one(const SearchArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((search_kernel<DS, REV, BF>), dim3(8 * a.chunks_per_xcd), dim3(kWave), 0, s, a);
+    hipLaunchKernelGGL((search_kernel<DS, REV, BF>), dim3(a.nchunks), dim3(kWave), 0, s, a);
 }
 
 template <int DS>
@@ -655,6 +699,7 @@ int launch_search(const float* aos, const float* frows, const float* fnorm, cons
     a.N = N;
     a.K = K;
     a.cap = cap;
+    a.room = min(cap, 4 * kWave);
     a.G = bf ? 0 : plan.grid_dim;
     a.res = bf ? 1 : plan.res;
     a.r2 = plan.r2;
@@ -674,7 +719,6 @@ int launch_search(const float* aos, const float* frows, const float* fnorm, cons
     a.thr_rel = (float)(2.0 * (DS + 8.0) * u);
     a.thr_abs = 1.0e-35f;
     a.nchunks = (N + kQB - 1) / kQB;
-    a.chunks_per_xcd = (a.nchunks + 7) / 8;
     if (plan.rev_order && !bf && DS == 4) {
         launch_one<4, true, false>(a, s);
     } else {
