@@ -63,9 +63,31 @@ __device__ __forceinline__ float key_d2(unsigned long long key) {
     return __uint_as_float((unsigned int)(key >> 32));
 }
 
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int mask) {
-    const unsigned int lo = (unsigned int)__shfl_xor((int)(unsigned int)v, mask);
-    const unsigned int hi = (unsigned int)__shfl_xor((int)(unsigned int)(v >> 32), mask);
+// Value of lane (lane ^ j) for j = 1, 2, 4, 8, 16, 32 without LDS traffic
+// where the hardware allows: DPP quad permutes (1, 2), a row rotation by 8
+// within 16-lane rows (8), the gfx950 row swaps (16, 32), and a swizzle (4).
+// j must fold to a constant (loops over it are fully unrolled).
+__device__ __forceinline__ unsigned xor_lane_u32(unsigned v, int j) {
+    const unsigned lane = threadIdx.x & (kWave - 1);
+    switch (j) {
+        case 1: return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+        case 2: return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+        case 4: return (unsigned)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);      // bitmask mode, xor 4
+        case 8: return __builtin_amdgcn_update_dpp(0u, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+        case 16: {
+            const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+            return (lane & 16) ? p[0] : p[1];
+        }
+        default: {
+            const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+            return (lane & 32) ? p[0] : p[1];
+        }
+    }
+}
+
+__device__ __forceinline__ unsigned long long xor_lane_u64(unsigned long long v, int j) {
+    const unsigned lo = xor_lane_u32((unsigned)v, j);
+    const unsigned hi = xor_lane_u32((unsigned)(v >> 32), j);
     return ((unsigned long long)hi << 32) | lo;
 }
 
@@ -75,46 +97,56 @@ __device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int
     return ((unsigned long long)hi << 32) | lo;
 }
 
-// Ascending bitonic sort of the 64*E keys held across one wave, x[e] being
-// element e*64 + lane.  Steps with a partner distance below 64 exchange through
-// lane shuffles; longer distances pair registers of the same lane.  No LDS and
-// no barriers.
+// Compare-exchange step of a bitonic network on 64*E keys held across one
+// wave (x[e] is element e*64 + lane): partner distance j, ascending where
+// bit k of the element index is clear (k = 0: ascending everywhere).
+template <int E>
+__device__ __forceinline__ void bitonic_step(unsigned long long (&x)[E], int k, int j) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if (j >= kWave) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int ep = e ^ (j / kWave);
+            if (ep > e) {
+                const bool up = ((e * kWave) & k) == 0;
+                const unsigned long long p = x[e], q = x[ep];
+                const bool sw = (p > q) == up;
+                x[e] = sw ? q : p;
+                x[ep] = sw ? p : q;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const unsigned long long y = xor_lane_u64(x[e], j);
+            const bool up = (((e * kWave) | lane) & k) == 0;
+            const bool keep_min = ((lane & j) == 0) == up;
+            const bool lt = x[e] < y;
+            x[e] = (lt == keep_min) ? x[e] : y;
+        }
+    }
+}
+
+template <int E>
+constexpr int log2_keys() { return 6 + (E == 1 ? 0 : E == 2 ? 1 : E == 4 ? 2 : 3); }
+
+// Ascending bitonic sort of the 64*E keys x[] (no LDS, no barriers).
 template <int E>
 __device__ __forceinline__ void wave_sort_u64(unsigned long long (&x)[E]) {
     static_assert(E == 1 || E == 2 || E == 4 || E == 8, "power-of-two register count");
-    constexpr int kLogP = 6 + (E == 1 ? 0 : E == 2 ? 1 : E == 4 ? 2 : 3);
-    const int lane = threadIdx.x & (kWave - 1);
     // affine loops over log2 distances so that both unroll fully and x[] stays in registers
 #pragma unroll
-    for (int lk = 1; lk <= kLogP; ++lk) {
-        const int k = 1 << lk;
+    for (int lk = 1; lk <= log2_keys<E>(); ++lk) {
 #pragma unroll
-        for (int lj = lk - 1; lj >= 0; --lj) {
-            const int j = 1 << lj;
-            if (j >= kWave) {
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const int ep = e ^ (j / kWave);
-                    if (ep > e) {
-                        const bool up = ((e * kWave) & k) == 0;
-                        const unsigned long long p = x[e], q = x[ep];
-                        const bool sw = (p > q) == up;
-                        x[e] = sw ? q : p;
-                        x[ep] = sw ? p : q;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    const unsigned long long y = shfl_xor_u64(x[e], j);
-                    const bool up = (((e * kWave) | lane) & k) == 0;
-                    const bool keep_min = ((lane & j) == 0) == up;
-                    const bool lt = x[e] < y;
-                    x[e] = (lt == keep_min) ? x[e] : y;
-                }
-            }
-        }
+        for (int lj = lk - 1; lj >= 0; --lj) bitonic_step<E>(x, 1 << lk, 1 << lj);
     }
+}
+
+// Ascending sort of a bitonic sequence of 64*E keys (the half-cleaner stages).
+template <int E>
+__device__ __forceinline__ void wave_bitonic_merge_u64(unsigned long long (&x)[E]) {
+#pragma unroll
+    for (int lj = log2_keys<E>() - 1; lj >= 0; --lj) bitonic_step<E>(x, 0, 1 << lj);
 }
 
 __device__ __forceinline__ int wave_min_i32(int v) {

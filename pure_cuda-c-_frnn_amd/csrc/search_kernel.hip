@@ -152,10 +152,10 @@ void search_kernel(SearchArgs a) {
     constexpr bool PREFETCH = DS <= 32;
     __shared__ __align__(16) float s_q[kQB * DS];
     __shared__ int s_cnt[kQB];
+    __shared__ int s_srt[kQB];       // sorted prefix length of each list
     __shared__ unsigned long long s_thr[kQB];
     __shared__ int s_qn[kQueueCap];
     __shared__ int s_qpos[kQueueCap];
-    __shared__ int s_qsize;
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points,
     // virtual stream positions [vbeg, vend), cell x and row-segment id
     __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing], r_x[kRing], r_seg[kRing];
@@ -191,9 +191,9 @@ void search_kernel(SearchArgs a) {
     }
     if (lane < kQB) {
         s_cnt[lane] = 0;
+        s_srt[lane] = 0;
         s_thr[lane] = make_key(a.r2, 0);
     }
-    if (lane == 0) s_qsize = 0;
     lds_sync();
     // B operand: this lane's half of query n's centred row, scaled by -2, plus
     // the norm column.  Rows of a chunk are the sorted points q0..q0+31.
@@ -220,36 +220,59 @@ void search_kernel(SearchArgs a) {
     const bool robust_q = __ballot(qvalid && !(qn2 < 1.0e37f)) != 0;
 
     long long c_shell = 0, c_hit = 0, c_acc = 0, c_ovf = 0, c_stream = 0;
+    int q_size = 0;                     // queue entries (wave-uniform)
 
-    // Sort query qn's candidate list in registers (wave_sort_u64 over the
-    // smallest power-of-two multiple of 64 holding it, ~0 filling the rest).
-    // Compaction keeps the K smallest keys and tightens the query's threshold
-    // to the K-th; the final pass writes the K smallest (padded with (r2, -1)).
-    auto select_sized = [&](auto e_const, int qn, int c, bool final_pass) __attribute__((always_inline)) {
-        constexpr int E = decltype(e_const)::value;
+    // Selection on query qn's candidate list.  A list keeps its first s_srt[qn]
+    // keys sorted (the K kept at the last compaction); later arrivals follow
+    // unsorted.  The new keys are sorted in registers (wave_sort_u64 over the
+    // smallest power-of-two multiple of 64 holding them, ~0 filling the rest)
+    // and their first P = 64*EK (>= K) are merged with the sorted prefix A:
+    // C[i] = min(A[i], B[P-1-i]) holds the P smallest of both and is bitonic,
+    // so the half-cleaner stages sort it.  Compaction keeps the K smallest and
+    // tightens the query's threshold to the K-th key; the final pass writes the
+    // K smallest (padded with (r2, -1)).
+    auto select_merge = [&](auto ek_const, auto en_const, int qn, int c, int m,
+                            bool final_pass) __attribute__((always_inline)) {
+        constexpr int EK = decltype(ek_const)::value;
+        constexpr int EN = decltype(en_const)::value;
         unsigned long long* L = lists + (size_t)qn * a.cap;
         // the list entries were stored by other lanes of this wave
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        unsigned long long x[E];
+        unsigned long long b[EN];
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int i = e * kWave + lane;
-            x[e] = (i < c) ? L[i] : ~0ull;
+        for (int e = 0; e < EN; ++e) {
+            const int i = m + e * kWave + lane;
+            b[e] = (i < c) ? L[i] : ~0ull;
         }
-        wave_sort_u64<E>(x);
+        wave_sort_u64<EN>(b);
+        unsigned long long x[EK];
+#pragma unroll
+        for (int e = 0; e < EK; ++e) x[e] = (e < EN) ? b[e] : ~0ull;
+        if (m > 0) {
+            // element i of C pairs A[i] with B[P-1-i]: register EK-1-e, lane 63-lane
+            unsigned long long cm[EK];
+#pragma unroll
+            for (int e = 0; e < EK; ++e) {
+                const int i = e * kWave + lane;
+                const unsigned long long av = (i < m) ? L[i] : ~0ull;
+                const unsigned long long rb = shfl_u64(x[EK - 1 - e], kWave - 1 - lane);
+                cm[e] = av < rb ? av : rb;
+            }
+#pragma unroll
+            for (int e = 0; e < EK; ++e) x[e] = cm[e];
+            wave_bitonic_merge_u64<EK>(x);
+        }
         if (final_pass) {
             const unsigned long long pad = make_key(a.r2, -1);
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
+            for (int e = 0; e < EK; ++e) {
                 const int i = e * kWave + lane;
                 if (i < a.K) L[i] = (i < c) ? x[e] : pad;
             }
-            // K may exceed the sorted span (few candidates, K > 64)
-            for (int i = E * kWave + lane; i < a.K; i += kWave) L[i] = pad;
         } else {
             const int keep = min(c, a.K);
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
+            for (int e = 0; e < EK; ++e) {
                 const int i = e * kWave + lane;
                 if (i < keep) L[i] = x[e];
             }
@@ -257,20 +280,31 @@ void search_kernel(SearchArgs a) {
                 const int ek = (a.K - 1) / kWave;
                 unsigned long long kth = x[0];
 #pragma unroll
-                for (int e = 1; e < E; ++e)
+                for (int e = 1; e < EK; ++e)
                     if (e == ek) kth = x[e];
                 kth = shfl_u64(kth, (a.K - 1) & (kWave - 1));
                 if (lane == 0) s_thr[qn] = kth;
             }
-            if (lane == 0) s_cnt[qn] = keep;
+            if (lane == 0) {
+                s_cnt[qn] = keep;
+                s_srt[qn] = keep;
+            }
         }
         lds_sync();
     };
     auto select_topk = [&](int qn, bool final_pass) __attribute__((always_inline)) {
         const int c = s_cnt[qn];
-        if (c <= kWave) select_sized(IntC<1>{}, qn, c, final_pass);
-        else if (c <= 2 * kWave) select_sized(IntC<2>{}, qn, c, final_pass);
-        else select_sized(IntC<4>{}, qn, c, final_pass);
+        const int m = s_srt[qn];
+        const int nn = c - m;
+        if (a.K <= kWave) {
+            if (nn <= kWave) select_merge(IntC<1>{}, IntC<1>{}, qn, c, m, final_pass);
+            else if (nn <= 2 * kWave) select_merge(IntC<1>{}, IntC<2>{}, qn, c, m, final_pass);
+            else select_merge(IntC<1>{}, IntC<4>{}, qn, c, m, final_pass);
+        } else {
+            if (nn <= kWave) select_merge(IntC<2>{}, IntC<1>{}, qn, c, m, final_pass);
+            else if (nn <= 2 * kWave) select_merge(IntC<2>{}, IntC<2>{}, qn, c, m, final_pass);
+            else select_merge(IntC<2>{}, IntC<4>{}, qn, c, m, final_pass);
+        }
     };
 
     // Exact re-evaluation of queue entries [base, base + count).  First every
@@ -303,8 +337,7 @@ void search_kernel(SearchArgs a) {
             }
         }
         lds_sync();
-        if (lane == 0) s_qsize = base;
-        lds_sync();
+        q_size = base;
     };
 
     // ---- candidate stream -------------------------------------------------
@@ -317,7 +350,7 @@ void search_kernel(SearchArgs a) {
     // Gather one tile of the stream into operand registers: the run lookup for
     // stream position v0 + n, the centred row half and the norm column.
     struct Tile {
-        float op[HD + 1];
+        float op[HD];
         int pos, x, seg, count;
     };
     auto gather = [&](int v0, int count, Tile& t) __attribute__((always_inline)) {
@@ -342,29 +375,38 @@ void search_kernel(SearchArgs a) {
             t.op[j] = vv.x;
             t.op[j + 1] = vv.y;
         }
-        t.op[HD] = (h == 0) ? (mvalid ? a.fnorm[t.pos] : 3.0e38f) : 1.0f;
     };
 
     // MFMA filter of one gathered tile: the 32 x 32 accumulator of filter values.
-    auto mfma_tile = [&](const Tile& t) __attribute__((always_inline)) {
+    // The norm column |p'|^2 is summed here from the row halves of lanes n and
+    // n + 32 (the filter's rounding bound holds for any summation order of the
+    // norm), which saves a random 4-byte load per candidate row; rows past the
+    // tile read as far away.  cand_norm returns the norm on h == 0 lanes.
+    auto mfma_tile = [&](const Tile& t, float& cand_norm) __attribute__((always_inline)) {
         floatx16 acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        float pn = 0.0f;
 #pragma unroll
-        for (int j = 0; j <= HD; ++j)
+        for (int j = 0; j < HD; ++j) {
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(t.op[j], bop[j], acc, 0, 0, 0);
-        return acc;
+            pn = fmaf(t.op[j], t.op[j], pn);
+        }
+        const float nrm = pn + __shfl_xor(pn, 32);
+        cand_norm = nrm;
+        const float last = (h == 0) ? (n < t.count ? nrm : 3.0e38f) : 1.0f;
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(last, bop[HD], acc, 0, 0, 0);
     };
 
     // Queue the tile's hits (filter value below the query's threshold, candidate
     // inside the query's shell) for exact re-evaluation.
-    auto hits_tile = [&](const Tile& t, const floatx16& acc) __attribute__((always_inline)) {
+    auto hits_tile = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
         if (h == 0) {
             t_pos[n] = t.pos;
             t_x[n] = t.x;
             t_seg[n] = t.seg;
         }
-        const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(t.op[HD] < 1.0e37f)) != 0);
+        const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
         // per group of four accumulator registers: does this lane hold a hit?
         bool gh[4];
 #pragma unroll
@@ -381,36 +423,45 @@ void search_kernel(SearchArgs a) {
         lds_sync();
         // All hits of the tile are queued first (at most 16 per lane, so the
         // queue never exceeds 63 + 1024 entries); the exact batches run after,
-        // when the accumulator registers are no longer live.
+        // when the accumulator registers are no longer live.  Queue slots come
+        // from a ballot prefix count, so pushes need no atomics.
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-            if (gh[g4]) {
+            if (__ballot(gh[g4]) == 0) continue;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int r = 4 * g4 + rr;
-                    if (!(acc[r] >= thr_f)) {
-                        // 32x32 accumulator layout: lane (n, h), register r holds
-                        // row 8*(r/4) + 4*h + r%4 (the candidate) of column n.
-                        const int row = 8 * g4 + 4 * h + rr;
-                        const int tseg = t_seg[row];
-                        const bool member = BF ? (tseg >= 0)
-                                               : (tseg == my_seg && abs(t_x[row] - x_n) <= 1);
-                        if (member && qvalid) {
-                            const int s = atomicAdd(&s_qsize, 1);
-                            if (s < kQueueCap) {
-                                s_qn[s] = n;
-                                s_qpos[s] = t_pos[row];
-                            } else {
-                                ++c_ovf;
-                            }
-                            ++c_hit;
+            for (int rr = 0; rr < 4; ++rr) {
+                const int r = 4 * g4 + rr;
+                bool push = false;
+                int cpos = 0;
+                if (gh[g4] && !(acc[r] >= thr_f)) {
+                    // 32x32 accumulator layout: lane (n, h), register r holds
+                    // row 8*(r/4) + 4*h + r%4 (the candidate) of column n.
+                    const int row = 8 * g4 + 4 * h + rr;
+                    const int tseg = t_seg[row];
+                    const bool member = BF ? (tseg >= 0)
+                                           : (tseg == my_seg && abs(t_x[row] - x_n) <= 1);
+                    push = member && qvalid;
+                    cpos = t_pos[row];
+                }
+                const unsigned long long pm = __ballot(push);
+                if (pm) {
+                    if (push) {
+                        const int s = q_size + (int)__builtin_amdgcn_mbcnt_hi(
+                                          (unsigned)(pm >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)pm, 0u));
+                        if (s < kQueueCap) {
+                            s_qn[s] = n;
+                            s_qpos[s] = cpos;
+                        } else {
+                            ++c_ovf;
                         }
+                        ++c_hit;
                     }
+                    q_size += __popcll(pm);
                 }
             }
         }
         lds_sync();
-        int qs = min(s_qsize, kQueueCap);
+        int qs = min(q_size, kQueueCap);
         while (qs >= kBatch) {
             process_batch(qs - kBatch, kBatch, false);
             qs -= kBatch;
@@ -429,12 +480,13 @@ void search_kernel(SearchArgs a) {
             const int vn = v_done + cur.count;
             const int an = v_total - vn;
             const bool has_next = an >= 32 || (final_pass && an > 0);
-            const floatx16 acc = mfma_tile(cur);
+            float cand_norm;
+            const floatx16 acc = mfma_tile(cur, cand_norm);
             Tile nxt;
             if constexpr (PREFETCH) {
                 if (has_next) gather(vn, min(32, an), nxt);
             }
-            hits_tile(cur, acc);
+            hits_tile(cur, acc, cand_norm);
             if (h == 0 && n == 0) c_stream += cur.count;
             v_done = vn;
             while (ring_tail < ring_head && r_vend[ring_tail & (kRing - 1)] <= v_done) ++ring_tail;
@@ -649,7 +701,7 @@ void search_kernel(SearchArgs a) {
     {
         // the last partial batch, then the final selection of every list
         // (one call site for both keeps a single inlined copy of the sorts)
-        const int qs = min(s_qsize, kQueueCap);
+        const int qs = min(q_size, kQueueCap);
 #pragma nounroll
         for (int pass = 0; pass < 2; ++pass) process_batch(0, pass == 0 ? qs : 0, pass == 1);
     }

@@ -29,3 +29,9 @@ def gpu_visible():
         return torch.cuda.device_count() > 0
     except Exception:
         return False
+
+
+# Count devices once at collection, before any test touches the GPU: a session
+# whose first torch.cuda call was is_available() inside a test saw no device
+# on the MI355X boxes, while every session that counted devices first did.
+gpu_visible()
