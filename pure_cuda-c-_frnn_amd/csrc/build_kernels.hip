@@ -187,47 +187,46 @@ __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ 
     write_rows(pts, N, D, ds, i, pos, aos, st, frows, fnorm);
 }
 
-// Per-axis statistics of coordinates g..D-1: partial sums (fp64) of x - x0
-// (x0 = the axis' first value, a shift that keeps the variance well
-// conditioned), minimum and maximum per block, reduced in a fixed order by
-// stats_setup_kernel.
-__global__ __launch_bounds__(256) void dim_stats_kernel(const float* __restrict__ pts, int N, int g, int D,
+// Per-coordinate statistics.  Block (b, d) reduces coordinate d over its
+// slice of the points: fp64 sums of x - x0 and (x - x0)^2 (x0 = the
+// coordinate's first value, a shift that keeps the variance well conditioned),
+// minimum and maximum.  stats_setup_kernel adds the slices in a fixed order.
+__global__ __launch_bounds__(256) void dim_stats_kernel(const float* __restrict__ pts, int N,
                                                         double* __restrict__ part) {
     __shared__ double s_sum[256], s_sq[256];
     __shared__ float s_mn[256], s_mx[256];
     const int t = threadIdx.x;
-    for (int d = g; d < D; ++d) {
-        const double pivot = pts[(size_t)d * N];
-        double sum = 0.0, sq = 0.0;
-        float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
-        for (long long i = (long long)blockIdx.x * 256 + t; i < N; i += 256LL * gridDim.x) {
-            const float v = pts[(size_t)d * N + i];
-            const double dv = (double)v - pivot;
-            sum += dv;
-            sq += dv * dv;
-            mn = fminf(mn, v);
-            mx = fmaxf(mx, v);
-        }
-        s_sum[t] = sum; s_sq[t] = sq; s_mn[t] = mn; s_mx[t] = mx;
-        __syncthreads();
-        for (int o = 128; o > 0; o >>= 1) {
-            if (t < o) {
-                s_sum[t] += s_sum[t + o];
-                s_sq[t] += s_sq[t + o];
-                s_mn[t] = fminf(s_mn[t], s_mn[t + o]);
-                s_mx[t] = fmaxf(s_mx[t], s_mx[t + o]);
-            }
-            __syncthreads();
-        }
-        if (t == 0) {
-            double* p = part + ((size_t)blockIdx.x * (D - g) + (d - g)) * 4;
-            p[0] = s_sum[0]; p[1] = s_sq[0]; p[2] = s_mn[0]; p[3] = s_mx[0];
+    const int d = blockIdx.y;
+    const float* col = pts + (size_t)d * N;
+    const double pivot = col[0];
+    double sum = 0.0, sq = 0.0;
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    for (long long i = (long long)blockIdx.x * 256 + t; i < N; i += 256LL * gridDim.x) {
+        const float v = col[i];
+        const double dv = (double)v - pivot;
+        sum += dv;
+        sq += dv * dv;
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+    }
+    s_sum[t] = sum; s_sq[t] = sq; s_mn[t] = mn; s_mx[t] = mx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (t < o) {
+            s_sum[t] += s_sum[t + o];
+            s_sq[t] += s_sq[t + o];
+            s_mn[t] = fminf(s_mn[t], s_mn[t + o]);
+            s_mx[t] = fmaxf(s_mx[t], s_mx[t + o]);
         }
         __syncthreads();
     }
+    if (t == 0) {
+        double* p = part + ((size_t)d * gridDim.x + blockIdx.x) * 4;
+        p[0] = s_sum[0]; p[1] = s_sq[0]; p[2] = s_mn[0]; p[3] = s_mx[0];
+    }
 }
 
-// Reduces the per-block partials (fixed order) into one DimStat per axis.  A
+// Adds the slices of each coordinate (fixed order) into one DimStat.  A
 // non-finite mean (NaN or infinite data) centres at 0 instead.
 __global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restrict__ pts,
                                                           const double* __restrict__ part, int nblk, int N, int D,
@@ -236,10 +235,13 @@ __global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restric
         const double pivot = pts[(size_t)d * N];
         double sum = 0.0, sq = 0.0;
         float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+        const double* p = part + (size_t)d * nblk * 4;
+#pragma unroll 8
         for (int b = 0; b < nblk; ++b) {
-            const double* p = part + ((size_t)b * D + d) * 4;
-            sum += p[0]; sq += p[1];
-            mn = fminf(mn, (float)p[2]); mx = fmaxf(mx, (float)p[3]);
+            sum += p[b * 4 + 0];
+            sq += p[b * 4 + 1];
+            mn = fminf(mn, (float)p[b * 4 + 2]);
+            mx = fmaxf(mx, (float)p[b * 4 + 3]);
         }
         const double shifted = sum / N;
         double var = sq / N - shifted * shifted;
@@ -308,12 +310,14 @@ __device__ __forceinline__ void pair_of(int p, int T, int& a, int& b) {
     b = a + p;
 }
 
-// Partial covariance sums of the projection terms: per block, the fp64 sum of
-// y_a * y_b (y = fl(x - mean), non-finite values as 0) for every pair a <= b.
-// A tile of 256 points is staged in LDS (row stride kMaxTerms + 1 so a wave's
-// reads of one point's terms hit distinct banks); threads split the pairs and,
-// with fewer than 256 pairs, the points of the tile.
-__global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts, int N,
+// Partial covariance sums of the projection terms over a sample of the input:
+// block b takes the 256 consecutive points starting at b * tile_stride (every
+// point when N <= kCovBlocks * 256), stages y = fl(x - mean) in LDS
+// (non-finite values as 0; row stride kMaxTerms + 1 so a wave's reads of one
+// point's terms hit distinct banks) and sums y_a * y_b in fp64 for every pair
+// a <= b.  Threads split the pairs and, with fewer than 256 pairs, the points.
+// The directions only steer the pruning, so a sample of >= 128K points serves.
+__global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts, int N, long long tile_stride,
                                                   const RefineInfo* __restrict__ ri, double* __restrict__ part) {
     constexpr int kStride = kMaxTerms + 1;
     __shared__ float s_y[256 * kStride];
@@ -334,29 +338,26 @@ __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts,
         slice = tid / P;
         np = 1;
     }
+    const long long i0 = (long long)blockIdx.x * tile_stride;
+    const int cnt = (int)max(0LL, min(256LL, (long long)N - i0));
+    for (int t = 0; t < T; ++t) {
+        float y = 0.0f;
+        if (tid < cnt) {
+            y = pts[(size_t)ri->coord[t] * N + i0 + tid] - ri->mean[t];
+            if (!(fabsf(y) <= 3.4e38f)) y = 0.0f;
+        }
+        s_y[tid * kStride + t] = y;
+    }
+    __syncthreads();
     double acc[3] = {0.0, 0.0, 0.0};
-    for (long long base = (long long)blockIdx.x * 256; base < N; base += 256LL * gridDim.x) {
-        const long long i = base + tid;
-        for (int t = 0; t < T; ++t) {
-            float y = 0.0f;
-            if (i < N) {
-                y = pts[(size_t)ri->coord[t] * N + i] - ri->mean[t];
-                if (!(fabsf(y) <= 3.4e38f)) y = 0.0f;
-            }
-            s_y[tid * kStride + t] = y;
-        }
-        __syncthreads();
-        const int cnt = (int)min(256LL, (long long)N - base);
 #pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            if (k < np) {
-                double s = 0.0;
-                for (int j = slice; j < cnt; j += slices)
-                    s = fma((double)s_y[j * kStride + pa[k]], (double)s_y[j * kStride + pb[k]], s);
-                acc[k] += s;
-            }
+    for (int k = 0; k < 3; ++k) {
+        if (k < np) {
+            double sum = 0.0;
+            for (int j = slice; j < cnt; j += slices)
+                sum = fma((double)s_y[j * kStride + pa[k]], (double)s_y[j * kStride + pb[k]], sum);
+            acc[k] = sum;
         }
-        __syncthreads();
     }
     double* out = part + (size_t)blockIdx.x * kMaxPairs;
     if (slices == 1) {
@@ -365,54 +366,80 @@ __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts,
         s_acc[tid] = acc[0];
         __syncthreads();
         if (tid < P) {
-            double s = 0.0;
-            for (int sl = 0; sl < slices; ++sl) s += s_acc[sl * P + tid];
-            out[tid] = s;
+            double sum = 0.0;
+            for (int sl = 0; sl < slices; ++sl) sum += s_acc[sl * P + tid];
+            out[tid] = sum;
         }
     }
 }
 
+// Wave sum of a double through the lane exchanges (no LDS).
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    for (int lj = 0; lj < 6; ++lj) {
+        const unsigned long long u = xor_lane_u64((unsigned long long)__double_as_longlong(v), 1 << lj);
+        v += __longlong_as_double((long long)u);
+    }
     return v;
 }
 __device__ __forceinline__ double wave_max_f64(double v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o));
+    for (int lj = 0; lj < 6; ++lj) {
+        const unsigned long long u = xor_lane_u64((unsigned long long)__double_as_longlong(v), 1 << lj);
+        v = fmax(v, __longlong_as_double((long long)u));
+    }
     return v;
 }
 
 // Reduces the covariance partials (fixed order), finds the top two principal
 // directions of the terms by subspace iteration with a final Rayleigh-Ritz
-// rotation (fp64, one wave, lane t = term t), and stores the weights scaled by
-// 1 - 2^-20 (so the fp32 weight vectors have norm < 1) with the sub-bin
-// geometry: each direction's bins span +-2.5 standard deviations of its
-// projections; points beyond clamp into the end bins.  Only quality depends on
-// these choices: the search's windows are exact for any weights of norm <= 1.
-__global__ __launch_bounds__(256) void refine_dirs_kernel(const double* __restrict__ part, int nblk, int N,
-                                                          RefineInfo* __restrict__ ri) {
+// rotation (fp64, one wave, lane t = term t; the iterate is broadcast through
+// LDS), and stores the weights scaled by 1 - 2^-20 (so the fp32 weight
+// vectors have norm < 1) with the sub-bin geometry: each direction's bins span
+// +-2.5 standard deviations of its projections; points beyond clamp into the
+// end bins.  Only quality depends on these choices: the search's windows are
+// exact for any weights of norm <= 1.
+__global__ __launch_bounds__(256) void refine_dirs_kernel(const double* __restrict__ part, int nblk,
+                                                          double nsamp, RefineInfo* __restrict__ ri) {
     __shared__ double s_C[kMaxTerms][kMaxTerms + 1];
+    __shared__ double s_v[2][kMaxTerms];
     const int tid = threadIdx.x;
     const int T = ri->terms;
     const int P = T * (T + 1) / 2;
     for (int p = tid; p < P; p += 256) {
-        double s = 0.0;
-        for (int b = 0; b < nblk; ++b) s += part[(size_t)b * kMaxPairs + p];
+        double sum = 0.0;
+#pragma unroll 8
+        for (int b = 0; b < nblk; ++b) sum += part[(size_t)b * kMaxPairs + p];
         int a, c;
         pair_of(p, T, a, c);
-        s /= (double)N;
-        s_C[a][c] = s;
-        s_C[c][a] = s;
+        sum /= nsamp;
+        s_C[a][c] = sum;
+        s_C[c][a] = sum;
     }
     __syncthreads();
     if (tid >= kWave) return;
     const int t = tid;
     const bool on = t < T;
-    auto matvec = [&](double v) {
-        double w = 0.0;
-        for (int j = 0; j < T; ++j) w = fma(s_C[on ? t : 0][j], __shfl(v, j), w);
-        return on ? w : 0.0;
+    // both products C v0, C v1 from one LDS broadcast of the iterate
+    auto matvec2 = [&](double& v0, double& v1) {
+        if (on) {
+            s_v[0][t] = v0;
+            s_v[1][t] = v1;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        double w0 = 0.0, w1 = 0.0;
+        for (int j = 0; j < T; ++j) {
+            const double c = s_C[on ? t : 0][j];
+            w0 = fma(c, s_v[0][j], w0);
+            w1 = fma(c, s_v[1][j], w1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        v0 = on ? w0 : 0.0;
+        v1 = on ? w1 : 0.0;
     };
     // orthonormal (x0, x1) spanning what (x0, x1) span; degenerate inputs fall
     // back to coordinate directions
@@ -448,12 +475,12 @@ __global__ __launch_bounds__(256) void refine_dirs_kernel(const double* __restri
         double v0 = on ? (t == 0 ? 1.0 : 0.0625 * (double)((t * 7) % 5 - 2)) : 0.0;
         double v1 = on ? (t == 1 ? 1.0 : 0.0625 * (double)((t * 3) % 7 - 3)) : 0.0;
         orthonormalise(v0, v1);
-        for (int it = 0; it < 48; ++it) {
-            v0 = matvec(v0);
-            v1 = matvec(v1);
+        for (int it = 0; it < 24; ++it) {
+            matvec2(v0, v1);
             orthonormalise(v0, v1);
         }
-        const double c0 = matvec(v0), c1 = matvec(v1);
+        double c0 = v0, c1 = v1;
+        matvec2(c0, c1);
         const double a = wave_sum_f64(v0 * c0), b = wave_sum_f64(v0 * c1), c = wave_sum_f64(v1 * c1);
         const double th = 0.5 * atan2(2.0 * b, a - c);
         const double cs = cos(th), sn = sin(th);
@@ -519,20 +546,34 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict_
     write_rows(pts, N, D, ds, i, i, aos, st, frows, fnorm);
 }
 
-// One thread per original query: reads its K sorted keys (contiguous, 16-byte
-// loads) and writes the SoA outputs, coalesced across the wave for each k.
+// Output transpose through LDS, 32 original queries per workgroup: the K keys
+// of each query's list (row inv[i] of the sorted order) are read with
+// consecutive threads on consecutive keys, then each k writes the 32 queries'
+// index and distance as one contiguous 128-byte segment of the SoA outputs.
+constexpr int kUnpermQ = 32;
 __global__ __launch_bounds__(256) void unpermute_kernel(const unsigned long long* __restrict__ lists,
                                                         int cap, const int* __restrict__ inv, int N,
                                                         int K, int* __restrict__ idxs,
                                                         float* __restrict__ dists) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= N) return;
-    const int sp = inv ? inv[i] : i;
-    const unsigned long long* L = lists + (size_t)sp * cap;
-    for (int k = 0; k < K; ++k) {
-        const unsigned long long key = L[k];
-        idxs[(size_t)k * N + i] = (int)(unsigned int)key;
-        dists[(size_t)k * N + i] = key_d2(key);
+    __shared__ unsigned long long s_t[kUnpermQ * (FRNN_MAX_K + 1)];
+    const int i0 = blockIdx.x * kUnpermQ;
+    const int nq = min(kUnpermQ, N - i0);
+    const int stride = K + 1;
+    for (int j = threadIdx.x; j < nq * K; j += blockDim.x) {
+        const int q = j / K;
+        const int k = j - q * K;
+        const int sp = inv ? inv[i0 + q] : i0 + q;
+        s_t[q * stride + k] = lists[(size_t)sp * cap + k];
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < K * kUnpermQ; j += blockDim.x) {
+        const int k = j / kUnpermQ;
+        const int q = j - k * kUnpermQ;
+        if (q < nq) {
+            const unsigned long long key = s_t[q * stride + k];
+            idxs[(size_t)k * N + i0 + q] = (int)(unsigned int)key;
+            dists[(size_t)k * N + i0 + q] = key_d2(key);
+        }
     }
 }
 
@@ -610,7 +651,7 @@ int launch_point_stats(const float* pts, int N, int D, void* stats_ws, hipStream
     const StatsLayout L = stats_layout(D);
     char* base = static_cast<char*>(stats_ws);
     double* part = reinterpret_cast<double*>(base + L.part);
-    hipLaunchKernelGGL(dim_stats_kernel, dim3(kStatBlocks), dim3(256), 0, s, pts, N, 0, D, part);
+    hipLaunchKernelGGL(dim_stats_kernel, dim3(kStatBlocks, D), dim3(256), 0, s, pts, N, part);
     hipLaunchKernelGGL(stats_setup_kernel, dim3(1), dim3(128), 0, s, pts, part, kStatBlocks, N, D,
                        reinterpret_cast<DimStat*>(base + L.dims));
     return launch_result();
@@ -630,8 +671,15 @@ int launch_refine(const float* pts, int N, int D, int g, long long cells, const 
     double* cov = reinterpret_cast<double*>(base + L.cov);
     int* subkey = reinterpret_cast<int*>(base + L.subkey);
     hipLaunchKernelGGL(refine_terms_kernel, dim3(1), dim3(64), 0, s, st, g, D, info);
-    hipLaunchKernelGGL(cov_kernel, dim3(kCovBlocks), dim3(256), 0, s, pts, N, info, cov);
-    hipLaunchKernelGGL(refine_dirs_kernel, dim3(1), dim3(256), 0, s, cov, kCovBlocks, N, info);
+    // covariance sample: kCovBlocks tiles of 256 consecutive points, evenly spaced
+    const long long tile_stride = N <= (long long)kCovBlocks * 256 ? 256 : (long long)N / kCovBlocks;
+    long long nsamp = 0;
+    for (int b = 0; b < kCovBlocks; ++b) {
+        const long long i0 = (long long)b * tile_stride;
+        nsamp += i0 < N ? (N - i0 < 256 ? N - i0 : 256) : 0;
+    }
+    hipLaunchKernelGGL(cov_kernel, dim3(kCovBlocks), dim3(256), 0, s, pts, N, tile_stride, info, cov);
+    hipLaunchKernelGGL(refine_dirs_kernel, dim3(1), dim3(256), 0, s, cov, kCovBlocks, (double)nsamp, info);
     int rc = launch_exclusive_scan(cnt, (int)cells + 1, bidx, scanpart, s, kBigCell);
     if (rc) return rc;
     rc = launch_fill_i32(subcnt, L.nsub, 0, s);
@@ -682,7 +730,8 @@ int launch_transpose(const float* pts, int N, int D, float* aos, const void* sta
 int launch_unpermute(const unsigned long long* lists, int cap, const int* inv, int N, int K, int* idxs,
                      float* dists, hipStream_t s) {
     if (N <= 0) return 0;
-    hipLaunchKernelGGL(unpermute_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, lists, cap, inv, N,
+    if (K < 1 || K > FRNN_MAX_K || cap < K) return 1;   // the LDS tile holds K <= FRNN_MAX_K keys
+    hipLaunchKernelGGL(unpermute_kernel, dim3(blocks_for(N, kUnpermQ)), dim3(256), 0, s, lists, cap, inv, N,
                        K, idxs, dists);
     return launch_result();
 }

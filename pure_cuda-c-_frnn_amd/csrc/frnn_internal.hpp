@@ -29,10 +29,10 @@ int scan_partials_count(int n);
 // cell to the sub-bins that intersect its queries' windows.
 constexpr int kBigCell = 256;
 constexpr int kSubBins = 1024;
-constexpr int kStatBlocks = 256;
+constexpr int kStatBlocks = 64;        // point slices per coordinate (statistics)
 constexpr int kMaxTerms = FRNN_REFINE_TERMS;
 constexpr int kMaxPairs = kMaxTerms * (kMaxTerms + 1) / 2;   // covariance entries
-constexpr int kCovBlocks = 256;
+constexpr int kCovBlocks = 512;         // sampled 256-point tiles (covariance)
 
 struct RefineInfo {
     int L;              // refinement directions (0 = none)

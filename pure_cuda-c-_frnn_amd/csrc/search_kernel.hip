@@ -568,7 +568,10 @@ void search_kernel(SearchArgs a) {
                 if (in_seg) my_seg = seg_id;
                 const int xlo = wave_min_i32(in_seg ? x_n : 0x7fffffff);
                 const int xhi = wave_max_i32(in_seg ? x_n : -1);
-                seg = __popcll(__ballot(row_n <= R) & 0xffffffffull);
+                // next segment: the queries past those with row <= R (rows are
+                // non-decreasing in the cell-sorted order); at least one step,
+                // so every wave terminates even on unsorted input
+                seg = max(seg + 1, (int)__popcll(__ballot(row_n <= R) & 0xffffffffull));
                 // segment bounding box on the gridded axes and the largest threshold
                 for (int d = 0; d < a.G; ++d) {
                     const float qd = qrow[d];

@@ -178,17 +178,20 @@ def test_refinement_orders_big_cells(name, N):
     W1 = np.array(ri.w1[:T], np.float64)
     assert np.linalg.norm(W0) < 1 and np.linalg.norm(W1) < 1
     assert abs(np.linalg.norm(W0) - 1) < 1e-5 and abs(np.linalg.norm(W1) - 1) < 1e-5 and abs(W0 @ W1) < 1e-5
-    # the directions span the top-2 principal subspace of the terms
+    # the directions capture (nearly) the variance of the top-2 principal
+    # subspace of the terms; the subspace itself is ill-defined when the second
+    # and third eigenvalues nearly tie (C3), and only pruning depends on it
     Y = (w.X[:, coord] - mean[coord]).astype(np.float64)
     C = Y.T @ Y / N
-    ev, V = np.linalg.eigh(C)
-    top = V[:, ::-1][:, :2]
-    span = np.stack([W0, W1], 1)
-    assert np.linalg.norm(span.T @ top) ** 2 > 2 * 0.98, (ev[::-1][:3])
-    # bins span +-2.5 standard deviations of each projection
+    ev = np.linalg.eigvalsh(C)[::-1]
+    captured = W0 @ C @ W0 + W1 @ C @ W1
+    assert captured >= 0.97 * (ev[0] + ev[1]), (captured, ev[:3])
+    # bins span +-2.5 standard deviations of each projection (the library
+    # estimates the covariance from a sample of >= 128K points: 3% tolerance)
     for wk, lok, invk, nbk in ((W0, ri.lo0, ri.inv0, ri.bins0), (W1, ri.lo1, ri.inv1, ri.bins1)):
         sg = np.sqrt(wk @ C @ wk)
-        assert abs(lok + 2.5 * sg) <= 1e-3 * sg and abs(invk * 5 * sg / nbk - 1) <= 1e-3
+        assert abs(lok + 2.5 * sg) <= 0.03 * 2.5 * sg and abs(invk * 5 * sg / nbk - 1) <= 0.03
+        assert lok == np.float32(lok) and abs(invk * (-2 * lok) / nbk - 1) < 1e-5
     # margin >= (T + 2) u |x - mean| over the input
     R = np.sqrt(np.sum(np.maximum(hi[coord].astype(np.float64) - mean[coord], mean[coord] - lo[coord].astype(np.float64)) ** 2))
     assert ri.margin >= (T + 2) * 2.0 ** -24 * R
