@@ -106,6 +106,8 @@ def main():
     ap.add_argument("--config", default="metric")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run three 256 MiB device copies (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -116,6 +118,17 @@ def main():
     import torch
     import frnn_cuda
     import frnn_workloads as W
+
+    if args.copy_probe:
+        n = 256 * 1024 * 1024 // 4
+        a = torch.ones(n, device="cuda:0")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        eprint(f"[bench] copy probe: 3 copies of {n * 4} bytes")
+        return
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     t_gen = time.perf_counter()

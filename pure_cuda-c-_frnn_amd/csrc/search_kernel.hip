@@ -141,20 +141,25 @@ __device__ __forceinline__ float exact_d2(const float* q, const float* __restric
 }
 
 // Small padded dimensions keep three waves per SIMD resident (register budget
-// 168); larger ones take what their operands need.
+// 168), larger ones two (256 VGPRs + AGPRs), so a second wave's MFMA chain can
+// overlap one wave's hit handling.
 template <int DS>
-struct WavesPerEU { static constexpr int value = DS <= 16 ? 3 : 1; };
+struct WavesPerEU { static constexpr int value = DS <= 16 ? 3 : 2; };
 
 template <int DS, bool REV, bool BF>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DS>::value)))
 void search_kernel(SearchArgs a) {
     constexpr int HD = DS / 2;
     constexpr bool PREFETCH = DS <= 32;
-    __shared__ __align__(16) float s_q[kQB * DS];
+    // The chunk's query rows: staged in LDS for DS <= 32; wider rows are read
+    // from the AoS array (the same 32 rows, cache resident), which keeps LDS
+    // small enough for two workgroups per SIMD.
+    constexpr bool kQueryLds = DS <= 32;
+    __shared__ __align__(16) float s_q[kQueryLds ? kQB * DS : 4];
     __shared__ int s_cnt[kQB];
     __shared__ int s_srt[kQB];       // sorted prefix length of each list
     __shared__ unsigned long long s_thr[kQB];
-    __shared__ int s_qn[kQueueCap];
+    __shared__ unsigned char s_qn[kQueueCap];
     __shared__ int s_qpos[kQueueCap];
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points,
     // virtual stream positions [vbeg, vend), cell x and row-segment id
@@ -178,7 +183,7 @@ void search_kernel(SearchArgs a) {
     const bool qvalid = n < nq;
     unsigned long long* const lists = a.lists + (size_t)q0 * a.cap;
 
-    {
+    if constexpr (kQueryLds) {
         const float* src = a.pts + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
         float* dst = s_q + n * DS + h * HD;
 #pragma unroll
@@ -189,6 +194,11 @@ void search_kernel(SearchArgs a) {
             dst[j + 1] = v.y;
         }
     }
+    // row of query qn (a valid query of the chunk)
+    auto query_row = [&](int qn) -> const float* {
+        if constexpr (kQueryLds) return s_q + qn * DS;
+        else return a.pts + (size_t)(q0 + qn) * DS;
+    };
     if (lane < kQB) {
         s_cnt[lane] = 0;
         s_srt[lane] = 0;
@@ -324,7 +334,7 @@ void search_kernel(SearchArgs a) {
         if (lane < count) {
             const int qn = s_qn[base + lane];
             const int pos = s_qpos[base + lane];
-            const float e = exact_d2<DS, REV>(s_q + qn * DS, a.pts + (size_t)pos * DS);
+            const float e = exact_d2<DS, REV>(query_row(qn), a.pts + (size_t)pos * DS);
             const int idx = BF ? pos : a.sorted_idx[pos];
             const unsigned long long key = make_key(e, idx);
             if (key < s_thr[qn]) {
@@ -449,7 +459,7 @@ void search_kernel(SearchArgs a) {
                         const int s = q_size + (int)__builtin_amdgcn_mbcnt_hi(
                                           (unsigned)(pm >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)pm, 0u));
                         if (s < kQueueCap) {
-                            s_qn[s] = n;
+                            s_qn[s] = (unsigned char)n;
                             s_qpos[s] = cpos;
                         } else {
                             ++c_ovf;
@@ -531,7 +541,7 @@ void search_kernel(SearchArgs a) {
         append_runs(0, lane == 0 ? a.N : 0, 0, 0);
         consume(true);
     } else {
-        const float* qrow = s_q + n * DS;
+        const float* qrow = query_row(qvalid ? n : 0);
         x_n = bin_coord(qrow[0], a.inv_cell, a.res);
         int row_n = 0;
         {
