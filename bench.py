@@ -42,23 +42,26 @@ def eprint(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_bytes(N, D, ds, g, C, refine):
+def build_bytes(N, D, ds, g, C, framed):
     """Algorithmic HBM bytes of each build kernel (4-byte ints and floats); ds is
-    the padded row length of the AoS and filter rows the reorder writes."""
+    the padded row length of the AoS and filter rows the reorder writes, C the
+    grid's cells (a frame's capacity for framed plans)."""
+    T = min(D, 32)
     b = {
         "zero_fill": 4 * (C + 1),
-        "bin_count": 4 * g * N + 8 * N + 8 * (C + 1),
         "stats": 4 * D * N,
+        "bin_count": 4 * (T if framed else g) * N + 8 * N + 8 * (C + 1),
         "scan": 8 * (C + 1),
         "reorder": 20 * N + 4 * D * N + 8 * ds * N + 4 * N,
     }
-    if refine:
-        # big-cell flags scan + covariance pass over the T projection terms + sub-bin
-        # count (cell, count, big-cell index, T terms; writes rank and key) + sub-bin
-        # fill and scan; the reorder also reads the keys
-        T = min(D - g, 32)
+    if framed:
+        # frame: covariance sample over the T projection terms (512 tiles of 256
+        # points); refine: big-cell flags scan + sub-bin count (cell, count,
+        # big-cell index, T terms; writes rank and key) + sub-bin fill and scan;
+        # the reorder also reads the keys
         nsub = (N // 256) * 1024 + 1
-        b["refine"] = 8 * (C + 1) + 4 * T * N + (20 + 4 * T) * N + 12 * nsub
+        b["frame"] = 4 * T * min(N, 512 * 256)
+        b["refine"] = 8 * (C + 1) + (20 + 4 * T) * N + 12 * nsub
         b["reorder"] += 4 * N
     return b
 
@@ -174,7 +177,7 @@ def main():
     search_s = stages["search"] / 1e3
     achieved = flops / search_s / 1e12
     traffic, traffic_src = traffic_from_profiles(args.config)
-    C = plan["cells"] if plan["path"] != "bruteforce" else 0
+    C = frnn_cuda.grid_cells(w.N, w.D, w.K, w.radius)
     alg_bytes = 8 * w.D * w.N + 4 * (C + 1) + 4 * w.N + 8 * w.K * w.N
     alg_gbs = alg_bytes / search_s / 1e9
     roofline = {"kernel": "search_kernel (neighbour search)", "bound": "mfma",
@@ -188,8 +191,9 @@ def main():
                              "frac": round(alg_gbs / HBM_PEAK_GBS, 5)}}
 
     if plan["path"] != "bruteforce":
-        bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"], plan["cells"],
-                         frnn_cuda.refine_workspace_bytes(w.N, w.D, w.K, w.radius) > 0)
+        bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"],
+                         frnn_cuda.grid_cells(w.N, w.D, w.K, w.radius),
+                         frnn_cuda.frame_workspace_bytes(w.N, w.D, w.K, w.radius) > 0)
     else:
         bb = {"stats": 4 * w.D * w.N, "reorder": 4 * w.D * w.N + 8 * frnn_cuda.aos_stride(w.D) * w.N + 4 * w.N}
     build = {}

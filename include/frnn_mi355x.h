@@ -67,28 +67,47 @@ typedef struct frnn_dim_stat {
     float mean, var, lo, hi;
 } frnn_dim_stat_t;
 
-/* Within-cell refinement descriptor; a refinement workspace starts with it.
- * Direction k (0 or 1) projects point x as the sequential fp32 fma chain
- *   s = 0;  s = fmaf(w_k[t], fl(x[coord[t]] - mean[t]), s)  for t = 0..terms-1
- * and its sub-bin is clamp(floor((s - lo_k) * inv_k), 0, bins_k - 1).  The
- * weights are the top principal directions of the non-grid coordinates
- * (norm < 1); margin bounds |computed s - exact w_k.(x - mean)| over every
- * finite input point, so two points within the radius have projections
- * closer than radius * (1 + 2^-15) + 2 * margin. */
-#define FRNN_REFINE_TERMS 32
-typedef struct frnn_refine_info {
-    int axes;          /* number of refinement directions (1 or 2) */
-    int bins0, bins1;  /* sub-bins per direction; bins0 * bins1 == 1024 */
-    int terms;         /* coordinates per projection, <= FRNN_REFINE_TERMS */
-    float lo0, lo1;    /* bin origin per direction */
-    float inv0, inv1;  /* bins per unit per direction (0: a single bin) */
-    float margin;      /* projection rounding bound */
-    int reserved[7];
-    int coord[FRNN_REFINE_TERMS];   /* term coordinates, highest variance first */
-    float mean[FRNN_REFINE_TERMS];  /* term centres (the point-statistics means) */
-    float w0[FRNN_REFINE_TERMS];    /* direction 0 weights */
-    float w1[FRNN_REFINE_TERMS];    /* direction 1 weights */
-} frnn_refine_info_t;
+/* Grid frame of first-coordinate plans (no reference counterpart); a frame
+ * workspace starts with it.  The result does not depend on the grid: every point
+ * within the radius of a query lies in the query's 3^g cell shell of any grid
+ * whose cells are at least the radius wide (plus rounding slack), so the engine
+ * grids the data along its own principal directions instead of the first g
+ * coordinates, which shrinks the shells of low-rank data several-fold.
+ *
+ * Projection of point x onto direction k (0 <= k < 6):
+ *   s = 0;  s = fmaf(dir[k][t], fl(x[coord[t]] - mean[t]), s)  for t = 0..terms-1
+ * (sequential fp32 fma chain; the weights of each direction have norm < 1 and the
+ * grid directions are orthonormal up to a 2^-18 shrink); margin bounds |computed -
+ * exact projection| over every finite input point.  Directions 0..grid_dim-1 are
+ * the grid axes: cell coordinate c_k = clamp(floor((s_k - lo[k]) * inv_h), 0,
+ * res[k] - 1) and cell id sum_k c_k * stride[k].  Directions 4 and 5 order the
+ * points inside cells of >= 256 points: sub-bin clamp(floor((s - rlo) * rinv),
+ * 0, bins - 1).  projected == 0 (infinite input) falls back to the first
+ * grid_dim raw coordinates with the plan's cell size and resolution. */
+#define FRNN_FRAME_TERMS 32
+#define FRNN_FRAME_DIRS 6
+typedef struct frnn_frame {
+    int grid_dim;          /* gridded directions g */
+    int cells;             /* prod res[k] */
+    int terms;             /* coordinates per projection, <= FRNN_FRAME_TERMS */
+    int axes;              /* refinement directions (0, 1 or 2) */
+    int projected;         /* 1: principal directions; 0: raw first coordinates */
+    int bins0, bins1;      /* refinement sub-bins per direction; bins0 * bins1 == 1024 */
+    int reserved0;
+    int res[4];            /* cells per grid direction */
+    int stride[4];         /* cell-id stride per grid direction, stride[0] == 1 */
+    float lo[4];           /* grid origin per direction */
+    float h, inv_h;        /* cell edge and fl(1/h) */
+    float margin;          /* projection rounding bound */
+    float slack;           /* binning rounding bound on a cell boundary */
+    float rlo0, rlo1;      /* refinement bin origin per direction */
+    float rinv0, rinv1;    /* refinement bins per unit (0: a single bin) */
+    float sigma[6];        /* standard deviation of the projections per direction */
+    int reserved1[2];
+    int coord[FRNN_FRAME_TERMS];               /* term coordinates, highest variance first */
+    float mean[FRNN_FRAME_TERMS];              /* term centres (the point-statistics means) */
+    float dir[FRNN_FRAME_DIRS][FRNN_FRAME_TERMS];   /* 0..3 grid, 4..5 refinement */
+} frnn_frame_t;
 
 /* ---- host-only helpers (no HIP call) ------------------------------------ */
 
@@ -142,10 +161,10 @@ int frnn_engine_set_stream(frnn_engine_t* engine, void* hip_stream);
 int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
 
 /* Per-stage HIP event timing (replaces the reference's FRNN_REPORT_OCCUPANCY
- * diagnostics, find_nbrs.cu:355-382).  Stages: 0 zero-fill, 1 bin+count,
- * 2 point statistics, 3 scan, 4 within-cell refinement, 5 reorder/transpose,
- * 6 neighbour search, 7 unpermute. */
-#define FRNN_NUM_STAGES 8
+ * diagnostics, find_nbrs.cu:355-382).  Stages: 0 zero-fill, 1 point
+ * statistics, 2 grid frame, 3 bin+count, 4 scan, 5 within-cell refinement,
+ * 6 reorder/transpose, 7 neighbour search, 8 unpermute. */
+#define FRNN_NUM_STAGES 9
 int frnn_engine_set_profiling(frnn_engine_t* engine, int enable);
 int frnn_engine_stage_times(const frnn_engine_t* engine, float* ms, int n);
 /* Work counters of the last profiled search: [0] shell candidates (sum over
@@ -160,13 +179,20 @@ int frnn_engine_counters(const frnn_engine_t* engine, long long* out, int n);
 /* ---- kernel launch seam (replaces run_*, frnn_engine.cu:9-20) ------------ */
 /* All pointers are device pointers; launches are asynchronous on `stream`. */
 
+/* Cell count a plan's grid uses: res^g, except for first-coordinate plans with
+ * dim > grid_dim (which have a frame): the frame's capacity
+ * max(min(max(N, 4096), FRNN_MAX_CELLS), res^g) (the frame picks its
+ * resolution to fit).
+ * Count arrays hold cells + 1 ints. */
+long long frnn_grid_cells(int N, int dim, const frnn_plan_t* plan);
+
 /* run_insert_points (insert_points.cu:45-88,167-174): zero d_cnt[0..cells],
- * bin every point on the first grid_dim coordinates (clamped to [0,res-1]),
- * d_cell_of[i] = row-major cell id, d_rank[i] = arrival slot in its cell,
- * d_cnt[c] = occupancy. */
+ * bin every point (without d_frame_ws: the first grid_dim coordinates, clamped
+ * to [0,res-1]; with a frame: its grid directions), d_cell_of[i] = cell id,
+ * d_rank[i] = arrival slot in its cell, d_cnt[c] = occupancy. */
 int frnn_launch_bin_count(const float* d_points_soa, int N, int grid_dim, int res,
-                          float inv_cell, long long cells, int* d_cell_of, int* d_rank,
-                          int* d_cnt, void* stream);
+                          float inv_cell, long long cells, const void* d_frame_ws, int* d_cell_of,
+                          int* d_rank, int* d_cnt, void* stream);
 
 /* thrust::exclusive_scan (frnn_engine.cu:91-94): d_out[i] = sum_{j<i} d_in[j]
  * for i < n.  d_partials holds frnn_scan_partials_count(n) ints. */
@@ -179,29 +205,31 @@ int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partia
 long long frnn_stats_workspace_bytes(int dim);
 int frnn_launch_point_stats(const float* d_points_soa, int N, int dim, void* d_stats_ws, void* stream);
 
-/* Within-cell refinement (no reference counterpart: the reference's within-cell
- * order is atomic arrival order, insert_points.cu:156-158, so any order is
- * admissible).  For first-coordinate plans with dim > grid_dim, cells holding
- * at least 256 points get 1024 sub-bins on the projections onto the two
- * principal directions of the (up to 32 highest-variance) non-grid
- * coordinates (frnn_refine_info_t; statistics from d_stats_ws); d_rank of
- * their points is replaced by the sub-bin arrival slot.  Needs frnn_refine_workspace_bytes() bytes at d_ws (0 bytes:
- * plan has no refinement, nothing to launch).  Run after the scan, before the
- * reorder. */
-long long frnn_refine_workspace_bytes(int N, int dim, const frnn_plan_t* plan);
+/* Grid frame and within-cell refinement of first-coordinate plans (no
+ * reference counterpart; frnn_frame_t).  frnn_frame_workspace_bytes() bytes at
+ * d_frame_ws (0: the plan has no frame).  frnn_launch_frame writes the frame
+ * (principal directions of the up to 32 highest-variance coordinates from a
+ * sampled covariance; needs the point statistics); run it before binning.
+ * frnn_launch_refine (after the scan) gives cells holding >= 256 points 1024
+ * sub-bins on the refinement directions and replaces d_rank of their points by
+ * the sub-bin arrival slot: the reference's within-cell order is atomic arrival
+ * order (insert_points.cu:156-158), so any order is admissible. */
+long long frnn_frame_workspace_bytes(int N, int dim, const frnn_plan_t* plan);
+int frnn_launch_frame(const float* d_points_soa, int N, int dim, const frnn_plan_t* plan,
+                      const void* d_stats_ws, void* d_frame_ws, void* stream);
 int frnn_launch_refine(const float* d_points_soa, int N, int dim, const frnn_plan_t* plan,
-                       const int* d_cell_of, const int* d_cnt, int* d_rank, const void* d_stats_ws,
-                       void* d_ws, void* stream);
+                       const int* d_cell_of, const int* d_cnt, int* d_rank, void* d_frame_ws,
+                       void* stream);
 
 /* run_counting_sort / run_counting_sort_aos3 (insert_points.cu:142-164,205-226):
  * pos = d_start[cell] + rank (+ the sub-bin offset inside refined cells);
  * d_sorted_idx[pos] = i; d_inv[i] = pos; AoS row pos of d_sorted_aos (stride
  * frnn_aos_stride(dim), zero padded) = point i.  With d_stats_ws, row pos of
  * d_frows gets fl(x - mean) and d_fnorm[pos] its squared norm (the MFMA filter
- * operands).  d_refine_ws and d_stats_ws may be NULL. */
+ * operands).  d_frame_ws and d_stats_ws may be NULL; cells as frnn_grid_cells. */
 int frnn_launch_reorder(const float* d_points_soa, int N, int dim, const int* d_cell_of,
                         const int* d_rank, const int* d_start, const int* d_cnt,
-                        const void* d_refine_ws, long long cells, int* d_sorted_idx, int* d_inv,
+                        const void* d_frame_ws, long long cells, int* d_sorted_idx, int* d_inv,
                         float* d_sorted_aos, const void* d_stats_ws, float* d_frows, float* d_fnorm,
                         void* stream);
 
@@ -214,15 +242,17 @@ int frnn_launch_transpose(const float* d_points_soa, int N, int dim, float* d_ao
  * (find_nbrs.cu:525-633, no_grid_frnn.cu:273-326): neighbour search over the
  * plan's path.  The MFMA filter streams d_frows/d_fnorm (written by the reorder
  * or transpose with statistics); exact distances use d_aos.  Grid paths read
- * the cell-sorted AoS points, d_sorted_idx and
- * d_start (cells+1 exclusive offsets), and the refinement tables when given;
- * brute force reads the transposed AoS points and ignores them.  Results: for sorted position s, entries
+ * the cell-sorted AoS points, d_sorted_idx, d_cell_of (cell id per original
+ * point), d_start (frnn_grid_cells + 1 exclusive offsets) and, for
+ * first-coordinate plans, the frame workspace; brute force reads the
+ * transposed AoS points and ignores them.  Results: for sorted position s, entries
  * d_lists[s*list_cap + k], k < K, hold ascending keys (bits(d2) << 32 | idx)
  * with padding (bits(r2) << 32 | 0xffffffff).  d_counters (5 u64: the
  * FRNN_NUM_COUNTERS work counters and a capacity-guard counter; may be NULL)
  * accumulates the counters. */
 int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float* d_fnorm,
-                          const int* d_sorted_idx, const int* d_start, const void* d_refine_ws,
+                          const int* d_sorted_idx, const int* d_cell_of, const int* d_start,
+                          const void* d_frame_ws,
                           int N, int dim, int K, const frnn_plan_t* plan,
                           unsigned long long* d_lists, int list_cap,
                           unsigned long long* d_counters, void* stream);

@@ -252,31 +252,30 @@ __global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restric
     }
 }
 
-// Picks the projection terms among coordinates g..D-1 (the kMaxTerms largest
-// variances, lower index on ties), their centres, the sub-bin split and the
-// projection rounding margin.  One thread.
+// Picks the projection terms of a frame: the kMaxTerms largest-variance
+// coordinates (lower index on ties), their centres, the direction count and
+// the projection rounding margin.  One thread.
 //
 // Margin: with y_t = fl(x_t - m_t) = (x_t - m_t)(1 + d_t), |d_t| <= u, the
 // sequential fma chain over T terms satisfies
 //   |s - sum w_t (x_t - m_t)| <= (gamma_T (1 + u) + u) sum |w_t| |x_t - m_t|
 //                             <= (T + 2) u |x - m|     (|w| <= 1, Cauchy-Schwarz)
 // and |x - m|^2 <= sum_t max(hi_t - m_t, m_t - lo_t)^2 over the input.  A
-// non-finite bound (infinite input) is stored as +inf: one sub-bin then.
-__global__ void refine_terms_kernel(const DimStat* __restrict__ st, int g, int D, RefineInfo* __restrict__ info) {
+// non-finite bound (infinite input) is stored as +inf; frame_dirs_kernel then
+// falls back to the raw first coordinates.
+__global__ void frame_terms_kernel(const DimStat* __restrict__ st, int g, int D, Frame* __restrict__ f) {
     if (threadIdx.x != 0) return;
-    const int nd = D - g;
-    const int T = nd < kMaxTerms ? nd : kMaxTerms;
+    const int T = D < kMaxTerms ? D : kMaxTerms;
     unsigned long long taken0 = 0ull, taken1 = 0ull;
     double R2 = 0.0;
     for (int t = 0; t < kMaxTerms; ++t) {
-        info->coord[t] = 0;
-        info->mean[t] = 0.0f;
-        info->w0[t] = 0.0f;
-        info->w1[t] = 0.0f;
+        f->coord[t] = 0;
+        f->mean[t] = 0.0f;
+        for (int k = 0; k < FRNN_FRAME_DIRS; ++k) f->dir[k][t] = 0.0f;
     }
     for (int t = 0; t < T; ++t) {
         int best = -1;
-        for (int d = g; d < D; ++d) {
+        for (int d = 0; d < D; ++d) {
             const unsigned long long bit = 1ull << (d & 63);
             if ((d < 64 ? taken0 : taken1) & bit) continue;
             if (best < 0 || st[d].var > st[best].var) best = d;
@@ -284,20 +283,20 @@ __global__ void refine_terms_kernel(const DimStat* __restrict__ st, int g, int D
         if (best < 64) taken0 |= 1ull << best;
         else taken1 |= 1ull << (best - 64);
         const DimStat s = st[best];
-        info->coord[t] = best;
-        info->mean[t] = s.mean;
+        f->coord[t] = best;
+        f->mean[t] = s.mean;
         const double e = fmax((double)s.hi - (double)s.mean, (double)s.mean - (double)s.lo);
         R2 += e * e;
     }
-    const int L = T >= 2 ? 2 : 1;
-    info->L = L;
-    info->nb1 = L == 2 ? 32 : kSubBins;
-    info->nb2 = L == 2 ? 32 : 1;
-    info->terms = T;
-    info->lo0 = info->lo1 = info->inv0 = info->inv1 = 0.0f;
+    f->g = g;
+    f->terms = T;
+    const int m = (g + 2 < T) ? g + 2 : T;   // grid + refinement directions
+    f->L = m - g;
+    f->nb1 = f->L == 2 ? 32 : kSubBins;
+    f->nb2 = f->L == 2 ? 32 : 1;
     const double E = (T + 2) * 5.9604644775390625e-08 * sqrt(R2) * (1.0 + 9.765625e-04);
-    info->margin = E < 1.0e30 ? (float)(E * (1.0 + 9.5367431640625e-07)) : __builtin_huge_valf();
-    for (int k = 0; k < 7; ++k) info->pad[k] = 0;
+    f->margin = E < 1.0e30 ? (float)(E * (1.0 + 9.5367431640625e-07)) : __builtin_huge_valf();
+    f->projected = 1;
 }
 
 // Pair p of the upper triangle (row-major over a <= b) of a T x T matrix.
@@ -318,12 +317,12 @@ __device__ __forceinline__ void pair_of(int p, int T, int& a, int& b) {
 // a <= b.  Threads split the pairs and, with fewer than 256 pairs, the points.
 // The directions only steer the pruning, so a sample of >= 128K points serves.
 __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts, int N, long long tile_stride,
-                                                  const RefineInfo* __restrict__ ri, double* __restrict__ part) {
+                                                  const Frame* __restrict__ f, double* __restrict__ part) {
     constexpr int kStride = kMaxTerms + 1;
     __shared__ float s_y[256 * kStride];
     __shared__ double s_acc[256];
     const int tid = threadIdx.x;
-    const int T = ri->terms;
+    const int T = f->terms;
     const int P = T * (T + 1) / 2;
     const int slices = P >= 256 ? 1 : 256 / P;
     int pa[3] = {0, 0, 0}, pb[3] = {0, 0, 0};
@@ -343,7 +342,7 @@ __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts,
     for (int t = 0; t < T; ++t) {
         float y = 0.0f;
         if (tid < cnt) {
-            y = pts[(size_t)ri->coord[t] * N + i0 + tid] - ri->mean[t];
+            y = pts[(size_t)f->coord[t] * N + i0 + tid] - f->mean[t];
             if (!(fabsf(y) <= 3.4e38f)) y = 0.0f;
         }
         s_y[tid * kStride + t] = y;
@@ -373,7 +372,7 @@ __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts,
     }
 }
 
-// Wave sum of a double through the lane exchanges (no LDS).
+// Wave sum / max of a double through the lane exchanges (no LDS).
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
     for (int lj = 0; lj < 6; ++lj) {
@@ -382,29 +381,41 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     }
     return v;
 }
-__device__ __forceinline__ double wave_max_f64(double v) {
-#pragma unroll
-    for (int lj = 0; lj < 6; ++lj) {
-        const unsigned long long u = xor_lane_u64((unsigned long long)__double_as_longlong(v), 1 << lj);
-        v = fmax(v, __longlong_as_double((long long)u));
-    }
-    return v;
-}
 
-// Reduces the covariance partials (fixed order), finds the top two principal
-// directions of the terms by subspace iteration with a final Rayleigh-Ritz
-// rotation (fp64, one wave, lane t = term t; the iterate is broadcast through
-// LDS), and stores the weights scaled by 1 - 2^-20 (so the fp32 weight
-// vectors have norm < 1) with the sub-bin geometry: each direction's bins span
-// +-2.5 standard deviations of its projections; points beyond clamp into the
-// end bins.  Only quality depends on these choices: the search's windows are
-// exact for any weights of norm <= 1.
-__global__ __launch_bounds__(256) void refine_dirs_kernel(const double* __restrict__ part, int nblk,
-                                                          double nsamp, RefineInfo* __restrict__ ri) {
+constexpr int kMaxDirs = FRNN_FRAME_DIRS;
+
+// Principal directions and geometry of a frame (fp64, one wave; lane t holds
+// component t of every direction).  The covariance partials are reduced in a
+// fixed order; m = g + L leading eigenvectors come from subspace iteration
+// (modified Gram-Schmidt, iterates broadcast through LDS) and a final
+// Rayleigh-Ritz step (cyclic Jacobi on the m x m projected matrix, one
+// thread).  Directions 0..g-1 become the grid axes, the next L the refinement
+// directions (slots 4, 5); weights are scaled by 1 - 2^-18, so the fp32 grid
+// directions stay orthonormal up to a shrink (|U d| <= |d| for any d) and
+// every direction has norm < 1.
+//
+// Grid geometry: origin -4 sigma per axis, cell edge
+//   h >= r (1 + 2^-12) + 2 margin + 2 slack,  slack = 2^-18 (4 sigma_max + h0),
+// enlarged until prod res <= cells_cap.  Two points within the radius (fp32
+// distance < r2, so |p - q| <= r (1 + 2^-15)) have computed projections closer
+// than r (1 + 2^-15) + 2 margin; with the rounding of the binning (bounded by
+// slack) their cell coordinates differ by at most one, so every neighbour lies
+// in the query's 3^g shell.  Refinement sub-bins span +-2.5 sigma.  An
+// infinite margin falls back to the raw first g coordinates with the plan's
+// cell size.
+__global__ __launch_bounds__(256) void frame_dirs_kernel(const double* __restrict__ part, int nblk,
+                                                         double nsamp, float radius, float cell_raw,
+                                                         float inv_cell_raw, int res_raw, int cells_cap,
+                                                         Frame* __restrict__ f) {
     __shared__ double s_C[kMaxTerms][kMaxTerms + 1];
-    __shared__ double s_v[2][kMaxTerms];
+    __shared__ double s_v[kMaxDirs][kMaxTerms];
+    __shared__ double s_H[kMaxDirs][kMaxDirs];
+    __shared__ double s_R[kMaxDirs][kMaxDirs];
+    __shared__ int s_perm[kMaxDirs];
     const int tid = threadIdx.x;
-    const int T = ri->terms;
+    const int T = f->terms;
+    const int g = f->g;
+    const int m = g + f->L;
     const int P = T * (T + 1) / 2;
     for (int p = tid; p < P; p += 256) {
         double sum = 0.0;
@@ -420,98 +431,257 @@ __global__ __launch_bounds__(256) void refine_dirs_kernel(const double* __restri
     if (tid >= kWave) return;
     const int t = tid;
     const bool on = t < T;
-    // both products C v0, C v1 from one LDS broadcast of the iterate
-    auto matvec2 = [&](double& v0, double& v1) {
-        if (on) {
-            s_v[0][t] = v0;
-            s_v[1][t] = v1;
-        }
+    auto lds_fence = [&]() {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        double w0 = 0.0, w1 = 0.0;
-        for (int j = 0; j < T; ++j) {
-            const double c = s_C[on ? t : 0][j];
-            w0 = fma(c, s_v[0][j], w0);
-            w1 = fma(c, s_v[1][j], w1);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        v0 = on ? w0 : 0.0;
-        v1 = on ? w1 : 0.0;
     };
-    // orthonormal (x0, x1) spanning what (x0, x1) span; degenerate inputs fall
-    // back to coordinate directions
-    auto orthonormalise = [&](double& x0, double& x1) {
-        double n0 = sqrt(wave_sum_f64(x0 * x0));
-        if (!(n0 > 1.0e-300 && n0 < 1.0e300)) {
-            x0 = (t == 0) ? 1.0 : 0.0;
-            n0 = 1.0;
-        }
-        x0 /= n0;
-        x1 -= wave_sum_f64(x1 * x0) * x0;
-        const double n1 = sqrt(wave_sum_f64(x1 * x1));
-        if (!(n1 > 1.0e-300 && n1 > 1.0e-14 * n0 && n1 < 1.0e300)) {
-            // e_k with k != argmax |x0| is never parallel to x0
-            const double m = fabs(x0);
-            const double mx = wave_max_f64(on ? m : -1.0);
-            const int kmax = __ffsll((long long)__ballot(on && m == mx)) - 1;
-            const int k = kmax == 0 ? 1 : 0;
-            x1 = (t == k) ? 1.0 : 0.0;
-            x1 -= wave_sum_f64(x1 * x0) * x0;
-            x1 /= sqrt(wave_sum_f64(x1 * x1));
-        } else {
-            x1 /= n1;
-        }
-    };
-    double u0, u1, l0, l1;
-    if (T == 1) {
-        u0 = (t == 0) ? 1.0 : 0.0;
-        u1 = 0.0;
-        l0 = s_C[0][0];
-        l1 = 0.0;
-    } else {
-        double v0 = on ? (t == 0 ? 1.0 : 0.0625 * (double)((t * 7) % 5 - 2)) : 0.0;
-        double v1 = on ? (t == 1 ? 1.0 : 0.0625 * (double)((t * 3) % 7 - 3)) : 0.0;
-        orthonormalise(v0, v1);
-        for (int it = 0; it < 24; ++it) {
-            matvec2(v0, v1);
-            orthonormalise(v0, v1);
-        }
-        double c0 = v0, c1 = v1;
-        matvec2(c0, c1);
-        const double a = wave_sum_f64(v0 * c0), b = wave_sum_f64(v0 * c1), c = wave_sum_f64(v1 * c1);
-        const double th = 0.5 * atan2(2.0 * b, a - c);
-        const double cs = cos(th), sn = sin(th);
-        u0 = cs * v0 + sn * v1;
-        u1 = cs * v1 - sn * v0;
-        l0 = a * cs * cs + 2.0 * b * sn * cs + c * sn * sn;
-        l1 = a * sn * sn - 2.0 * b * sn * cs + c * cs * cs;
-    }
-    constexpr double kShrink = 1.0 - 9.5367431640625e-07;   // 1 - 2^-20
-    if (on) {
-        ri->w0[t] = (float)(u0 * kShrink);
-        ri->w1[t] = ri->L > 1 ? (float)(u1 * kShrink) : 0.0f;
-    }
-    if (t == 0) {
-        const bool exact = ri->margin < 1.0e30f;
-        float lo[2] = {0.0f, 0.0f}, inv[2] = {0.0f, 0.0f};
-        const double lam[2] = {l0, l1};
-        const int nb[2] = {ri->nb1, ri->nb2};
-        for (int k = 0; k < ri->L; ++k) {
-            const double sg = sqrt(fmax(lam[k], 0.0));
-            const double iv = (double)nb[k] / (5.0 * sg);
-            if (exact && sg > 0.0 && iv < 1.0e30) {
-                lo[k] = (float)(-2.5 * sg);
-                inv[k] = (float)iv;
+    double v[kMaxDirs];
+#pragma unroll
+    for (int j = 0; j < kMaxDirs; ++j)
+        v[j] = (on && j < m) ? ((t == j) ? 1.0 : 0.0625 * (double)((t * (2 * j + 3)) % 7 - 3)) : 0.0;
+    // modified Gram-Schmidt; a collapsed vector is replaced by the first
+    // coordinate direction with a substantial residual (one exists: j < m <= T)
+    auto orthonormalise = [&]() {
+#pragma unroll
+        for (int j = 0; j < kMaxDirs; ++j) {
+            if (j >= m) break;
+            const double n_in = sqrt(wave_sum_f64(v[j] * v[j]));
+#pragma unroll
+            for (int k = 0; k < kMaxDirs; ++k)
+                if (k < j) v[j] -= wave_sum_f64(v[j] * v[k]) * v[k];
+            double nrm = sqrt(wave_sum_f64(v[j] * v[j]));
+            if (!(nrm > 1.0e-300 && nrm > 1.0e-12 * n_in && nrm < 1.0e300)) {
+                for (int c = 0; c < T; ++c) {
+                    double cand = (t == c) ? 1.0 : 0.0;
+#pragma unroll
+                    for (int k = 0; k < kMaxDirs; ++k)
+                        if (k < j) cand -= wave_sum_f64(cand * v[k]) * v[k];
+                    const double nc = sqrt(wave_sum_f64(cand * cand));
+                    if (nc > 0.1) {
+                        v[j] = cand;
+                        nrm = nc;
+                        break;
+                    }
+                }
             }
+            v[j] /= nrm;
         }
-        ri->lo0 = lo[0];
-        ri->lo1 = lo[1];
-        ri->inv0 = inv[0];
-        ri->inv1 = inv[1];
+    };
+    // w_j = C v_j for all directions, from one LDS broadcast of the iterate
+    auto matvec = [&](double (&w)[kMaxDirs]) {
+#pragma unroll
+        for (int j = 0; j < kMaxDirs; ++j)
+            if (on && j < m) s_v[j][t] = v[j];
+        lds_fence();
+#pragma unroll
+        for (int j = 0; j < kMaxDirs; ++j) w[j] = 0.0;
+        for (int k = 0; k < T; ++k) {
+            const double c = s_C[on ? t : 0][k];
+#pragma unroll
+            for (int j = 0; j < kMaxDirs; ++j)
+                if (j < m) w[j] = fma(c, s_v[j][k], w[j]);
+        }
+        lds_fence();
+#pragma unroll
+        for (int j = 0; j < kMaxDirs; ++j)
+            if (!on) w[j] = 0.0;
+    };
+    orthonormalise();
+    for (int it = 0; it < 24; ++it) {
+        double w[kMaxDirs];
+        matvec(w);
+#pragma unroll
+        for (int j = 0; j < kMaxDirs; ++j) v[j] = w[j];
+        orthonormalise();
     }
+    // Rayleigh-Ritz: H = V^T C V, eigen-decomposed by cyclic Jacobi on lane 0
+    {
+        double w[kMaxDirs];
+        matvec(w);
+#pragma unroll
+        for (int j = 0; j < kMaxDirs; ++j)
+#pragma unroll
+            for (int k = 0; k < kMaxDirs; ++k) {
+                if (j < m && k < m) {
+                    const double hjk = wave_sum_f64(v[j] * w[k]);
+                    if (t == 0) s_H[j][k] = hjk;
+                }
+            }
+    }
+    lds_fence();
+    if (t == 0) {
+        for (int j = 0; j < m; ++j)
+            for (int k = 0; k < m; ++k) s_R[j][k] = (j == k) ? 1.0 : 0.0;
+        for (int j = 0; j < m; ++j)
+            for (int k = j + 1; k < m; ++k) {
+                const double sym = 0.5 * (s_H[j][k] + s_H[k][j]);
+                s_H[j][k] = sym;
+                s_H[k][j] = sym;
+            }
+        for (int sweep = 0; sweep < 50; ++sweep) {
+            double off = 0.0, dia = 0.0;
+            for (int j = 0; j < m; ++j) {
+                dia += s_H[j][j] * s_H[j][j];
+                for (int k = j + 1; k < m; ++k) off += s_H[j][k] * s_H[j][k];
+            }
+            if (!(off > 1.0e-30 * dia) || !(off > 1.0e-300)) break;
+            for (int pp = 0; pp < m; ++pp)
+                for (int q = pp + 1; q < m; ++q) {
+                    const double apq = s_H[pp][q];
+                    if (!(fabs(apq) > 1.0e-300)) continue;
+                    const double th = (s_H[q][q] - s_H[pp][pp]) / (2.0 * apq);
+                    const double tt = (th >= 0.0 ? 1.0 : -1.0) / (fabs(th) + sqrt(th * th + 1.0));
+                    const double cs = 1.0 / sqrt(tt * tt + 1.0), sn = tt * cs;
+                    for (int k = 0; k < m; ++k) {   // columns pp, q of H
+                        const double hkp = s_H[k][pp], hkq = s_H[k][q];
+                        s_H[k][pp] = cs * hkp - sn * hkq;
+                        s_H[k][q] = sn * hkp + cs * hkq;
+                    }
+                    for (int k = 0; k < m; ++k) {   // rows pp, q of H
+                        const double hpk = s_H[pp][k], hqk = s_H[q][k];
+                        s_H[pp][k] = cs * hpk - sn * hqk;
+                        s_H[q][k] = sn * hpk + cs * hqk;
+                    }
+                    for (int k = 0; k < m; ++k) {   // eigenvector columns
+                        const double rkp = s_R[k][pp], rkq = s_R[k][q];
+                        s_R[k][pp] = cs * rkp - sn * rkq;
+                        s_R[k][q] = sn * rkp + cs * rkq;
+                    }
+                }
+        }
+        // eigenvalues descending (ties: lower index first)
+        for (int j = 0; j < m; ++j) s_perm[j] = j;
+        for (int j = 0; j < m; ++j)
+            for (int k = j + 1; k < m; ++k)
+                if (s_H[s_perm[k]][s_perm[k]] > s_H[s_perm[j]][s_perm[j]]) {
+                    const int tmp = s_perm[j];
+                    s_perm[j] = s_perm[k];
+                    s_perm[k] = tmp;
+                }
+    }
+    lds_fence();
+    constexpr double kShrink = 1.0 - 3.814697265625e-06;   // 1 - 2^-18
+#pragma unroll
+    for (int j = 0; j < kMaxDirs; ++j) {
+        if (j >= m) break;
+        const int col = s_perm[j];
+        double u = 0.0;
+#pragma unroll
+        for (int k = 0; k < kMaxDirs; ++k)
+            if (k < m) u = fma(s_R[k][col], v[k], u);
+        const int slot = j < g ? j : kRefDir0 + (j - g);
+        if (on) f->dir[slot][t] = (float)(u * kShrink);
+        if (t == 0) f->sigma[slot] = (float)sqrt(fmax(s_H[col][col], 0.0));
+    }
+    if (t != 0) return;
+    // ---- geometry (one thread) ----
+    const bool exact = f->margin < 1.0e30f;
+    if (!exact) {
+        // infinite input: grid on the raw first g coordinates, no refinement
+        f->projected = 0;
+        f->L = 0;
+        f->margin = 0.0f;
+        f->slack = 0.0f;
+        f->h = cell_raw;
+        f->inv_h = inv_cell_raw;
+        int stride = 1;
+        for (int d = 0; d < kFrameGrid; ++d) {
+            f->res[d] = d < g ? res_raw : 1;
+            f->lo[d] = 0.0f;
+            f->stride[d] = stride;
+            if (d < g) stride *= res_raw;
+        }
+        f->cells = stride;
+        f->rlo0 = f->rlo1 = f->rinv0 = f->rinv1 = 0.0f;
+        return;
+    }
+    double sig[kFrameGrid];
+    double smax = 0.0;
+    for (int d = 0; d < kFrameGrid; ++d) {
+        sig[d] = d < g ? (double)f->sigma[d] : 0.0;
+        smax = fmax(smax, sig[d]);
+    }
+    const double h0 = (double)radius * (1.0 + 2.44140625e-04) + 2.0 * (double)f->margin;
+    // slack as stored (fp32, rounded up by the 2^-10 factor), so h covers it
+    const double slack = (double)(float)(3.814697265625e-06 * (4.0 * smax + h0) * (1.0 + 9.765625e-04));
+    // start where no axis needs more than 2^20 cells, then grow h by 1/16
+    // until the grid fits (at most ~700 steps from there; a bounded loop with
+    // a single-cell fallback keeps the thread finite whatever the input)
+    double h = fmax(h0 + 2.0 * slack, 8.0 * smax / 1048576.0);
+    int res[kFrameGrid];
+    long long cells = 0;
+    for (int pass = 0; pass < 4096 && !(cells >= 1 && cells <= cells_cap); ++pass) {
+        if (pass > 0) h *= 1.0625;
+        cells = 1;
+        for (int d = 0; d < kFrameGrid; ++d) {
+            double rd = d < g ? ceil(8.0 * sig[d] / h) : 1.0;
+            rd = fmin(fmax(rd, 1.0), 1048576.0);
+            res[d] = (int)rd;
+            cells *= res[d];
+        }
+    }
+    if (!(cells >= 1 && cells <= cells_cap))
+        for (int d = 0; d < kFrameGrid; ++d) res[d] = 1;
+    // store h rounded up and inv_h rounded down, so the binning never
+    // narrows a cell below h
+    // (both positive: one ulp up / down is the bit pattern +- 1)
+    float hf = (float)h;
+    if ((double)hf < h) hf = __uint_as_float(__float_as_uint(hf) + 1u);
+    float ih = (float)(1.0 / (double)hf);
+    if ((double)ih > 1.0 / (double)hf) ih = __uint_as_float(__float_as_uint(ih) - 1u);
+    f->h = hf;
+    f->inv_h = ih;
+    f->slack = (float)slack;
+    int stride = 1;
+    for (int d = 0; d < kFrameGrid; ++d) {
+        f->res[d] = res[d];
+        f->lo[d] = d < g ? (float)(-4.0 * sig[d]) : 0.0f;
+        f->stride[d] = stride;
+        stride *= res[d];
+    }
+    f->cells = stride;
+    // refinement sub-bins over +-2.5 sigma of each refinement direction
+    float rlo[2] = {0.0f, 0.0f}, rinv[2] = {0.0f, 0.0f};
+    const int nb[2] = {f->nb1, f->nb2};
+    for (int k = 0; k < f->L; ++k) {
+        const double sg = (double)f->sigma[kRefDir0 + k];
+        const double iv = (double)nb[k] / (5.0 * sg);
+        if (sg > 0.0 && iv < 1.0e30) {
+            rlo[k] = (float)(-2.5 * sg);
+            rinv[k] = (float)iv;
+        }
+    }
+    f->rlo0 = rlo[0];
+    f->rlo1 = rlo[1];
+    f->rinv0 = rinv[0];
+    f->rinv1 = rinv[1];
+}
+
+// Binning on a frame's grid directions: projections (or, without a
+// projection, the raw first g coordinates), clamped cell coordinates, cell id
+// and the arrival slot in the cell.
+__global__ __launch_bounds__(256) void bin_frame_kernel(const float* __restrict__ pts, int N,
+                                                        const Frame* __restrict__ f, int cells,
+                                                        int* __restrict__ cell_of, int* __restrict__ rank,
+                                                        int* __restrict__ cnt) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    const int g = f->g;
+    float s[kFrameGrid];
+    if (f->projected) {
+        frame_project(f, 0, [&](int d) { return pts[(size_t)d * N + i]; }, s);
+    } else {
+#pragma unroll
+        for (int d = 0; d < kFrameGrid; ++d) s[d] = d < g ? pts[(size_t)d * N + i] : 0.0f;
+    }
+    int c = 0;
+#pragma unroll
+    for (int d = 0; d < kFrameGrid; ++d)
+        if (d < g) c += sub_bin(s[d], f->lo[d], f->inv_h, f->res[d]) * f->stride[d];
+    c = c < cells ? c : cells - 1;   // the frame fits `cells`; a mismatched count array stays in bounds
+    cell_of[i] = c;
+    rank[i] = atomicAdd(&cnt[c], 1);
 }
 
 // Sub-bin key and counting inside big cells; the arrival slot in the sub-bin
@@ -520,18 +690,18 @@ __global__ __launch_bounds__(256) void sub_count_kernel(const float* __restrict_
                                                         const int* __restrict__ cell_of,
                                                         const int* __restrict__ cnt,
                                                         const int* __restrict__ bidx,
-                                                        const RefineInfo* __restrict__ ref,
+                                                        const Frame* __restrict__ f,
                                                         int* __restrict__ subcnt, int* __restrict__ rank,
                                                         int* __restrict__ subkey) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
     const int c = cell_of[i];
     if (cnt[c] < kBigCell) return;
-    float s0, s1;
-    refine_project(ref, [&](int d) { return pts[(size_t)d * N + i]; }, s0, s1);
-    const int q1 = sub_bin(s0, ref->lo0, ref->inv0, ref->nb1);
-    const int q2 = ref->L > 1 ? sub_bin(s1, ref->lo1, ref->inv1, ref->nb2) : 0;
-    const int key = q1 * ref->nb2 + q2;
+    float s[2];
+    frame_project(f, kRefDir0, [&](int d) { return pts[(size_t)d * N + i]; }, s);
+    const int q1 = sub_bin(s[0], f->rlo0, f->rinv0, f->nb1);
+    const int q2 = f->L > 1 ? sub_bin(s[1], f->rlo1, f->rinv1, f->nb2) : 0;
+    const int key = q1 * f->nb2 + q2;
     subkey[i] = key;
     rank[i] = atomicAdd(&subcnt[(size_t)bidx[c] * kSubBins + key], 1);
 }
@@ -598,11 +768,18 @@ int launch_fill_i32(int* p, long long n, int v, hipStream_t s) {
     return launch_result();
 }
 
-int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, int* cell_of, int* rank,
-                     int* cnt, hipStream_t s) {
+int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, const void* frame_ws,
+                     int cells, int* cell_of, int* rank, int* cnt, hipStream_t s) {
     if (N <= 0) return 0;
-    hipLaunchKernelGGL(bin_count_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, g, res,
-                       inv_cell, cell_of, rank, cnt);
+    if (frame_ws) {
+        if (cells < 1) return 1;
+        const Frame* f = reinterpret_cast<const Frame*>(static_cast<const char*>(frame_ws));
+        hipLaunchKernelGGL(bin_frame_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, f, cells,
+                           cell_of, rank, cnt);
+    } else {
+        hipLaunchKernelGGL(bin_count_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, g, res,
+                           inv_cell, cell_of, rank, cnt);
+    }
     return launch_result();
 }
 
@@ -620,12 +797,12 @@ int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStre
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-RefineLayout refine_layout(int N, int D, long long cells) {
-    RefineLayout L{};
+FrameLayout frame_layout(int N, int D, long long cells) {
+    FrameLayout L{};
     L.max_big = N / kBigCell;
     L.nsub = L.max_big * kSubBins + 1;
     size_t off = 0;
-    L.info = off;     off = align256(off + sizeof(RefineInfo));
+    L.frame = off;    off = align256(off + sizeof(Frame));
     L.bidx = off;     off = align256(off + (size_t)(cells + 1) * sizeof(int));
     L.subcnt = off;   off = align256(off + (size_t)L.nsub * sizeof(int));
     L.substart = off; off = align256(off + (size_t)L.nsub * sizeof(int));
@@ -657,20 +834,15 @@ int launch_point_stats(const float* pts, int N, int D, void* stats_ws, hipStream
     return launch_result();
 }
 
-int launch_refine(const float* pts, int N, int D, int g, long long cells, const int* cell_of, const int* cnt,
-                  int* rank, const void* stats_ws, void* ws, hipStream_t s) {
-    if (N <= 0 || D <= g) return 0;
-    const RefineLayout L = refine_layout(N, D, cells);
+int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long long cells,
+                 const void* stats_ws, void* ws, hipStream_t s) {
+    if (N <= 0 || !has_frame(plan, D)) return 0;
+    const FrameLayout L = frame_layout(N, D, cells);
     char* base = static_cast<char*>(ws);
-    RefineInfo* info = reinterpret_cast<RefineInfo*>(base + L.info);
-    int* bidx = reinterpret_cast<int*>(base + L.bidx);
-    int* subcnt = reinterpret_cast<int*>(base + L.subcnt);
-    int* substart = reinterpret_cast<int*>(base + L.substart);
-    int* scanpart = reinterpret_cast<int*>(base + L.scanpart);
+    Frame* f = reinterpret_cast<Frame*>(base + L.frame);
     const DimStat* st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
     double* cov = reinterpret_cast<double*>(base + L.cov);
-    int* subkey = reinterpret_cast<int*>(base + L.subkey);
-    hipLaunchKernelGGL(refine_terms_kernel, dim3(1), dim3(64), 0, s, st, g, D, info);
+    hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(64), 0, s, st, plan.grid_dim, D, f);
     // covariance sample: kCovBlocks tiles of 256 consecutive points, evenly spaced
     const long long tile_stride = N <= (long long)kCovBlocks * 256 ? 256 : (long long)N / kCovBlocks;
     long long nsamp = 0;
@@ -678,29 +850,44 @@ int launch_refine(const float* pts, int N, int D, int g, long long cells, const 
         const long long i0 = (long long)b * tile_stride;
         nsamp += i0 < N ? (N - i0 < 256 ? N - i0 : 256) : 0;
     }
-    hipLaunchKernelGGL(cov_kernel, dim3(kCovBlocks), dim3(256), 0, s, pts, N, tile_stride, info, cov);
-    hipLaunchKernelGGL(refine_dirs_kernel, dim3(1), dim3(256), 0, s, cov, kCovBlocks, (double)nsamp, info);
+    hipLaunchKernelGGL(cov_kernel, dim3(kCovBlocks), dim3(256), 0, s, pts, N, tile_stride, f, cov);
+    hipLaunchKernelGGL(frame_dirs_kernel, dim3(1), dim3(256), 0, s, cov, kCovBlocks, (double)nsamp,
+                       plan.cell_size, plan.cell_size, plan.inv_cell, plan.res, (int)cells, f);
+    return launch_result();
+}
+
+int launch_refine(const float* pts, int N, int D, long long cells, const int* cell_of, const int* cnt,
+                  int* rank, void* ws, hipStream_t s) {
+    if (N <= 0) return 0;
+    const FrameLayout L = frame_layout(N, D, cells);
+    char* base = static_cast<char*>(ws);
+    const Frame* f = reinterpret_cast<const Frame*>(base + L.frame);
+    int* bidx = reinterpret_cast<int*>(base + L.bidx);
+    int* subcnt = reinterpret_cast<int*>(base + L.subcnt);
+    int* substart = reinterpret_cast<int*>(base + L.substart);
+    int* scanpart = reinterpret_cast<int*>(base + L.scanpart);
+    int* subkey = reinterpret_cast<int*>(base + L.subkey);
     int rc = launch_exclusive_scan(cnt, (int)cells + 1, bidx, scanpart, s, kBigCell);
     if (rc) return rc;
     rc = launch_fill_i32(subcnt, L.nsub, 0, s);
     if (rc) return rc;
     hipLaunchKernelGGL(sub_count_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, cell_of, cnt,
-                       bidx, info, subcnt, rank, subkey);
+                       bidx, f, subcnt, rank, subkey);
     rc = launch_exclusive_scan(subcnt, L.nsub, substart, scanpart, s);
     if (rc) return rc;
     return launch_result();
 }
 
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,
-                   const int* cnt, const void* refine_ws, long long cells, int* sorted_idx, int* inv,
+                   const int* cnt, const void* frame_ws, long long cells, int* sorted_idx, int* inv,
                    float* aos, const void* stats_ws, float* frows, float* fnorm, hipStream_t s) {
     if (N <= 0) return 0;
     const int* subkey = nullptr;
     const int* bidx = nullptr;
     const int* substart = nullptr;
-    if (refine_ws) {
-        const RefineLayout L = refine_layout(N, D, cells);
-        const char* base = static_cast<const char*>(refine_ws);
+    if (frame_ws) {
+        const FrameLayout L = frame_layout(N, D, cells);
+        const char* base = static_cast<const char*>(frame_ws);
         subkey = reinterpret_cast<const int*>(base + L.subkey);
         bidx = reinterpret_cast<const int*>(base + L.bidx);
         substart = reinterpret_cast<const int*>(base + L.substart);

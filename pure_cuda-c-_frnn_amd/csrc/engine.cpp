@@ -99,9 +99,9 @@ struct frnn_engine {
     float* out_dist = nullptr;
     float* aos = nullptr;
     size_t aos_bytes = 0;
-    void* refine_ws = nullptr;    // within-cell refinement tables
-    size_t refine_bytes = 0;
-    void* stats_ws = nullptr;     // per-coordinate statistics (filter centre, refinement axes)
+    void* frame_ws = nullptr;     // grid frame and within-cell refinement tables
+    size_t frame_bytes = 0;
+    void* stats_ws = nullptr;     // per-coordinate statistics (filter centre, frame terms)
     size_t stats_bytes = 0;
     float* frows = nullptr;       // centred filter rows, stride aos_stride(dim)
     size_t frows_bytes = 0;
@@ -125,7 +125,7 @@ namespace {
 void release(frnn_engine* e) {
     void* bufs[] = {e->cell_of, e->rank, e->sorted_idx, e->inv, e->cnt, e->start, e->partials,
                     e->counters, e->out_idx, e->out_dist, e->aos, e->lists, e->h2d_points,
-                    e->refine_ws, e->stats_ws, e->frows, e->fnorm};
+                    e->frame_ws, e->stats_ws, e->frows, e->fnorm};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (auto& ev : e->ev)
@@ -154,7 +154,14 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
 
     hipStream_t s = e->stream;
     const bool grid = plan.path != FRNN_PATH_BRUTEFORCE;
-    const void* refine = nullptr;
+    const bool framed = grid && frnn::has_frame(plan, dim);
+    const long long cells = grid ? frnn::grid_cells(N, dim, plan) : 0;
+    const void* frame = nullptr;
+    if (framed) {
+        ST_TRY(grow((char**)&e->frame_ws, &e->frame_bytes, frnn::frame_layout(N, dim, cells).total,
+                    "allocating the grid frame"));
+        frame = e->frame_ws;
+    }
     if (e->profiling) {
         ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * kCounterSlots, 0, s),
                              "clearing counters"));
@@ -164,55 +171,57 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
         if (e->profiling) HIP_TRY(hipEventRecord(e->ev[i], s), "event record");
         return FRNN_OK;
     };
-    // stage 0: zero-fill, 1: bin+count (frnn_engine.cu:89-90, 159-160)
-    if (grid) ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, plan.cells + 1, 0, s), "zero-fill cells"));
+    // stage 0: zero-fill the counts (frnn_engine.cu:89-90)
+    if (grid) ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, cells + 1, 0, s), "zero-fill cells"));
     ST_TRY(mark(1));
-    if (grid)
-        ST_TRY(launch_status(frnn::launch_bin_count(d_pts, N, plan.grid_dim, plan.res, plan.inv_cell,
-                                                    e->cell_of, e->rank, e->cnt, s),
-                             "bin/count launch"));
-    ST_TRY(mark(2));
-    // stage 2: per-coordinate statistics (filter centre, refinement axes)
+    // stage 1: per-coordinate statistics (filter centre, frame terms)
     ST_TRY(launch_status(frnn::launch_point_stats(d_pts, N, dim, e->stats_ws, s), "statistics launch"));
+    ST_TRY(mark(2));
+    // stage 2: grid frame of first-coordinate plans with D > g
+    if (framed)
+        ST_TRY(launch_status(frnn::launch_frame(d_pts, N, dim, plan, cells, e->stats_ws, e->frame_ws, s),
+                             "frame launch"));
     ST_TRY(mark(3));
-    // stage 3: exclusive scan of the counts (thrust::exclusive_scan, frnn_engine.cu:91-94)
+    // stage 3: bin + count (run_insert_points, frnn_engine.cu:159-160)
     if (grid)
-        ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)plan.cells + 1, e->start,
-                                                         e->partials, s),
-                             "scan launch"));
+        ST_TRY(launch_status(frnn::launch_bin_count(d_pts, N, plan.grid_dim, plan.res, plan.inv_cell, frame,
+                                                    (int)cells, e->cell_of, e->rank, e->cnt, s),
+                             "bin/count launch"));
     ST_TRY(mark(4));
-    // stage 4: within-cell refinement of big cells (first-coordinate grids with D > g)
-    if (grid && frnn::refine_axes(plan, dim) > 0) {
-        const frnn::RefineLayout L = frnn::refine_layout(N, dim, plan.cells);
-        ST_TRY(grow((char**)&e->refine_ws, &e->refine_bytes, L.total, "allocating refinement tables"));
-        refine = e->refine_ws;
-        ST_TRY(launch_status(frnn::launch_refine(d_pts, N, dim, plan.grid_dim, plan.cells, e->cell_of,
-                                                 e->cnt, e->rank, e->stats_ws, e->refine_ws, s),
-                             "refinement launch"));
-    }
+    // stage 4: exclusive scan of the counts (thrust::exclusive_scan, frnn_engine.cu:91-94)
+    if (grid)
+        ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)cells + 1, e->start, e->partials, s),
+                             "scan launch"));
     ST_TRY(mark(5));
-    // stage 5: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
+    // stage 5: within-cell refinement of big cells (framed plans)
+    if (framed)
+        ST_TRY(launch_status(frnn::launch_refine(d_pts, N, dim, cells, e->cell_of, e->cnt, e->rank,
+                                                 e->frame_ws, s),
+                             "refinement launch"));
+    ST_TRY(mark(6));
+    // stage 6: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
     // brute force, the AoS copy; both also write the filter rows
     if (grid)
         ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start, e->cnt,
-                                                  refine, plan.cells, e->sorted_idx, e->inv, e->aos,
+                                                  frame, cells, e->sorted_idx, e->inv, e->aos,
                                                   e->stats_ws, e->frows, e->fnorm, s),
                              "reorder launch"));
     else
         ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, e->stats_ws, e->frows, e->fnorm, s),
                              "transpose launch"));
-    ST_TRY(mark(6));
-    // stage 6: neighbour search
-    ST_TRY(launch_status(frnn::launch_search(e->aos, e->frows, e->fnorm, grid ? e->sorted_idx : nullptr,
-                                             grid ? e->start : nullptr, refine, N, dim, K, plan,
-                                             e->lists, cap, e->profiling ? e->counters : nullptr, s),
-                         "search launch"));
     ST_TRY(mark(7));
-    // stage 7: results to the original query order (ScatterToOrigKernel)
+    // stage 7: neighbour search
+    ST_TRY(launch_status(frnn::launch_search(e->aos, e->frows, e->fnorm, grid ? e->sorted_idx : nullptr,
+                                             grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
+                                             N, dim, K, plan, e->lists, cap,
+                                             e->profiling ? e->counters : nullptr, s),
+                         "search launch"));
+    ST_TRY(mark(8));
+    // stage 8: results to the original query order (ScatterToOrigKernel)
     ST_TRY(launch_status(frnn::launch_unpermute(e->lists, cap, grid ? e->inv : nullptr, N, K,
                                                 e->out_idx, e->out_dist, s),
                          "unpermute launch"));
-    ST_TRY(mark(8));
+    ST_TRY(mark(9));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
     if (e->profiling) {
         for (int i = 0; i < FRNN_NUM_STAGES; ++i)
@@ -461,18 +470,25 @@ int frnn_engine_counters(const frnn_engine_t* e, long long* out, int n) {
 
 // ---- kernel launch seam ----------------------------------------------------
 
-int frnn_launch_bin_count(const float* d_pts, int N, int grid_dim, int res, float inv_cell,
-                          long long cells, int* d_cell_of, int* d_rank, int* d_cnt, void* stream) {
+long long frnn_grid_cells(int N, int dim, const frnn_plan_t* plan) {
+    if (!plan || N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return -1;
+    if (plan->path != FRNN_PATH_GRID_FIRST && plan->path != FRNN_PATH_GRID_FULL) return 0;
+    return frnn::grid_cells(N, dim, *plan);
+}
+
+int frnn_launch_bin_count(const float* d_pts, int N, int grid_dim, int res, float inv_cell, long long cells,
+                          const void* d_frame_ws, int* d_cell_of, int* d_rank, int* d_cnt, void* stream) {
     if (N < 0 || grid_dim < 1 || grid_dim > 9 || res < 1 || cells < 1 || cells > FRNN_MAX_CELLS)
         return fail(FRNN_ERR_INVALID_ARGUMENT, "bad bin/count geometry");
-    if (ipow_sat(res, grid_dim, (long long)4e18) != cells)
+    if (!d_frame_ws && ipow_sat(res, grid_dim, (long long)4e18) != cells)
         return fail(FRNN_ERR_INVALID_ARGUMENT, "cells must equal res^grid_dim");
+    if (d_frame_ws && grid_dim > 4) return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame has at most 4 grid axes");
     if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_cnt))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
     hipStream_t s = (hipStream_t)stream;
     ST_TRY(launch_status(frnn::launch_fill_i32(d_cnt, cells + 1, 0, s), "zero-fill cells"));
-    return launch_status(frnn::launch_bin_count(d_pts, N, grid_dim, res, inv_cell, d_cell_of, d_rank,
-                                                d_cnt, s),
+    return launch_status(frnn::launch_bin_count(d_pts, N, grid_dim, res, inv_cell, d_frame_ws, (int)cells,
+                                                d_cell_of, d_rank, d_cnt, s),
                          "bin/count launch");
 }
 
@@ -495,35 +511,53 @@ int frnn_launch_point_stats(const float* d_pts, int N, int dim, void* d_stats_ws
                          "statistics launch");
 }
 
-long long frnn_refine_workspace_bytes(int N, int dim, const frnn_plan_t* plan) {
+long long frnn_frame_workspace_bytes(int N, int dim, const frnn_plan_t* plan) {
     if (!plan || N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return -1;
-    if (frnn::refine_axes(*plan, dim) == 0 || N == 0) return 0;
-    return (long long)frnn::refine_layout(N, dim, plan->cells).total;
+    if (N == 0 || !frnn::has_frame(*plan, dim)) return 0;
+    return (long long)frnn::frame_layout(N, dim, frnn::grid_cells(N, dim, *plan)).total;
+}
+
+static int check_frame_plan(int N, int dim, const frnn_plan_t* plan) {
+    if (!plan || N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N, dim or plan");
+    if (!frnn::has_frame(*plan, dim)) return fail(FRNN_ERR_INVALID_ARGUMENT, "the plan has no frame");
+    if (plan->grid_dim < 1 || plan->grid_dim > 4 || plan->res < 1 || plan->cells < 1 ||
+        plan->cells > FRNN_MAX_CELLS || ipow_sat(plan->res, plan->grid_dim, (long long)4e18) != plan->cells)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "inconsistent grid plan");
+    return FRNN_OK;
+}
+
+int frnn_launch_frame(const float* d_pts, int N, int dim, const frnn_plan_t* plan, const void* d_stats_ws,
+                      void* d_frame_ws, void* stream) {
+    ST_TRY(check_frame_plan(N, dim, plan));
+    if (N == 0) return FRNN_OK;
+    if (!d_pts || !d_stats_ws || !d_frame_ws) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    return launch_status(frnn::launch_frame(d_pts, N, dim, *plan, frnn::grid_cells(N, dim, *plan), d_stats_ws,
+                                            d_frame_ws, (hipStream_t)stream),
+                         "frame launch");
 }
 
 int frnn_launch_refine(const float* d_pts, int N, int dim, const frnn_plan_t* plan, const int* d_cell_of,
-                       const int* d_cnt, int* d_rank, const void* d_stats_ws, void* d_ws, void* stream) {
-    if (!plan || N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad refine arguments");
-    if (frnn::refine_axes(*plan, dim) == 0 || N == 0) return FRNN_OK;
-    if (plan->cells < 1 || plan->cells > FRNN_MAX_CELLS) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad cell count");
-    if (!d_pts || !d_cell_of || !d_cnt || !d_rank || !d_stats_ws || !d_ws)
+                       const int* d_cnt, int* d_rank, void* d_frame_ws, void* stream) {
+    ST_TRY(check_frame_plan(N, dim, plan));
+    if (N == 0) return FRNN_OK;
+    if (!d_pts || !d_cell_of || !d_cnt || !d_rank || !d_frame_ws)
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    return launch_status(frnn::launch_refine(d_pts, N, dim, plan->grid_dim, plan->cells, d_cell_of, d_cnt, d_rank,
-                                             d_stats_ws, d_ws, (hipStream_t)stream),
+    return launch_status(frnn::launch_refine(d_pts, N, dim, frnn::grid_cells(N, dim, *plan), d_cell_of, d_cnt,
+                                             d_rank, d_frame_ws, (hipStream_t)stream),
                          "refinement launch");
 }
 
 int frnn_launch_reorder(const float* d_pts, int N, int dim, const int* d_cell_of, const int* d_rank,
-                        const int* d_start, const int* d_cnt, const void* d_refine_ws, long long cells,
+                        const int* d_start, const int* d_cnt, const void* d_frame_ws, long long cells,
                         int* d_sorted_idx, int* d_inv, float* d_sorted_aos, const void* d_stats_ws,
                         float* d_frows, float* d_fnorm, void* stream) {
     if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
     if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_start || !d_sorted_idx || !d_inv || !d_sorted_aos))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    if (d_refine_ws && (!d_cnt || cells < 1 || cells > FRNN_MAX_CELLS))
-        return fail(FRNN_ERR_INVALID_ARGUMENT, "refinement needs counts and the cell count");
+    if (d_frame_ws && (!d_cnt || cells < 1 || cells > FRNN_MAX_CELLS))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame needs the counts and the cell count");
     if (d_stats_ws && (!d_frows || !d_fnorm)) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need both outputs");
-    return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_cnt, d_refine_ws,
+    return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_cnt, d_frame_ws,
                                               cells, d_sorted_idx, d_inv, d_sorted_aos, d_stats_ws, d_frows,
                                               d_fnorm, (hipStream_t)stream),
                          "reorder launch");
@@ -540,25 +574,27 @@ int frnn_launch_transpose(const float* d_pts, int N, int dim, float* d_aos, cons
 }
 
 int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float* d_fnorm,
-                          const int* d_sorted_idx, const int* d_start, const void* d_refine_ws, int N, int dim,
-                          int K, const frnn_plan_t* plan, unsigned long long* d_lists, int list_cap,
-                          unsigned long long* d_counters, void* stream) {
+                          const int* d_sorted_idx, const int* d_cell_of, const int* d_start,
+                          const void* d_frame_ws, int N, int dim, int K, const frnn_plan_t* plan,
+                          unsigned long long* d_lists, int list_cap, unsigned long long* d_counters,
+                          void* stream) {
     if (!plan) return fail(FRNN_ERR_INVALID_ARGUMENT, "null plan");
     ST_TRY(frnn_validate(0, N, dim, K, plan->cell_size));
     if (plan->path == FRNN_PATH_EMPTY || N == 0) return FRNN_OK;
     if (list_cap < frnn::list_capacity(K)) return fail(FRNN_ERR_INVALID_ARGUMENT, "list_cap too small");
     const bool grid = plan->path != FRNN_PATH_BRUTEFORCE;
-    if (!d_aos || !d_frows || !d_fnorm || !d_lists || (grid && (!d_sorted_idx || !d_start)))
+    if (!d_aos || !d_frows || !d_fnorm || !d_lists || (grid && (!d_sorted_idx || !d_cell_of || !d_start)))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
     if (grid && (plan->grid_dim < 1 || plan->grid_dim > 9 || plan->grid_dim > dim || plan->res < 1 ||
                  ipow_sat(plan->res, plan->grid_dim, (long long)4e18) != plan->cells ||
                  plan->cells > FRNN_MAX_CELLS))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "inconsistent grid plan");
     if (plan->rev_order && (!grid || dim != 3)) return fail(FRNN_ERR_INVALID_ARGUMENT, "reversed order is D=3 grid only");
-    if (d_refine_ws && frnn::refine_axes(*plan, dim) == 0)
-        return fail(FRNN_ERR_INVALID_ARGUMENT, "refinement tables given for a plan without refinement");
-    return launch_status(frnn::launch_search(d_aos, d_frows, d_fnorm, d_sorted_idx, d_start, d_refine_ws, N, dim,
-                                             K, *plan, d_lists, list_cap, d_counters, (hipStream_t)stream),
+    if (d_frame_ws && !frnn::has_frame(*plan, dim))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame given for a plan without one");
+    return launch_status(frnn::launch_search(d_aos, d_frows, d_fnorm, d_sorted_idx, d_cell_of, d_start,
+                                             d_frame_ws, N, dim, K, *plan, d_lists, list_cap, d_counters,
+                                             (hipStream_t)stream),
                          "search launch");
 }
 

@@ -35,22 +35,20 @@ __device__ __forceinline__ int sub_bin(float x, float lo, float inv, int nb) {
     return (int)f;
 }
 
-// Projections of a point onto both refinement directions: for each, the
+// Projections of a point onto frame directions k0 .. k0+M-1: for each, the
 // sequential fma chain over the terms of fl(x[coord[t]] - mean[t]) weighted by
-// w0[t] / w1[t] (w1 is zero with one direction), with coord(c) returning
-// coordinate c of the point.  The build (sub-bin keys) and the search (query
-// windows) both use it; each value is within RefineInfo::margin of the exact
+// dir[k][t], with coord(c) returning coordinate c of the point.  Binning and
+// the search both use it; each value is within Frame::margin of the exact
 // projection.
-template <class Coord>
-__device__ __forceinline__ void refine_project(const RefineInfo* __restrict__ ri, Coord coord, float& s0,
-                                               float& s1) {
-    s0 = 0.0f;
-    s1 = 0.0f;
-    const int T = ri->terms;
+template <int M, class Coord>
+__device__ __forceinline__ void frame_project(const Frame* __restrict__ f, int k0, Coord coord, float (&s)[M]) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) s[m] = 0.0f;
+    const int T = f->terms;
     for (int t = 0; t < T; ++t) {
-        const float y = coord(ri->coord[t]) - ri->mean[t];
-        s0 = fmaf(ri->w0[t], y, s0);
-        s1 = fmaf(ri->w1[t], y, s1);
+        const float y = coord(f->coord[t]) - f->mean[t];
+#pragma unroll
+        for (int m = 0; m < M; ++m) s[m] = fmaf(f->dir[k0 + m][t], y, s[m]);
     }
 }
 

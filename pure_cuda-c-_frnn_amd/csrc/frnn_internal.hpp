@@ -21,56 +21,71 @@ inline int list_capacity(int K) { return K + 128; }
 
 int scan_partials_count(int n);
 
-// ---- within-cell refinement -------------------------------------------------
-// Cells holding at least kBigCell points are ordered internally by a 2-D
-// sub-bin key on the projections onto the two principal directions of the
-// non-grid coordinates (one direction when only one non-grid coordinate
-// exists), kSubBins sub-bins per big cell.  The search then restricts each big
-// cell to the sub-bins that intersect its queries' windows.
+// ---- grid frame and within-cell refinement ----------------------------------
+// First-coordinate plans grid the data on its principal directions (Frame);
+// cells holding at least kBigCell points are ordered internally by a 32 x 32
+// sub-bin key on the next two principal directions, kSubBins sub-bins per big
+// cell, and the search restricts each big cell to the sub-bins that intersect
+// its queries' windows.
 constexpr int kBigCell = 256;
 constexpr int kSubBins = 1024;
 constexpr int kStatBlocks = 64;        // point slices per coordinate (statistics)
-constexpr int kMaxTerms = FRNN_REFINE_TERMS;
+constexpr int kMaxTerms = FRNN_FRAME_TERMS;
 constexpr int kMaxPairs = kMaxTerms * (kMaxTerms + 1) / 2;   // covariance entries
 constexpr int kCovBlocks = 512;         // sampled 256-point tiles (covariance)
+constexpr int kFrameGrid = 4;           // grid directions of a frame (slots 0..3)
+constexpr int kRefDir0 = 4;             // refinement directions (slots 4, 5)
 
-struct RefineInfo {
-    int L;              // refinement directions (0 = none)
-    int nb1, nb2;       // sub-bins per direction, nb1 * nb2 == kSubBins
-    int terms;          // coordinates per projection
-    float lo0, lo1;     // bin origin per direction
-    float inv0, inv1;   // bins per unit per direction
-    float margin;       // bound on the projection rounding of any finite point
-    int pad[7];
+struct Frame {
+    int g, cells, terms, L;             // grid directions, cells, projection terms, refinement dirs
+    int projected;                      // 0: raw first coordinates (infinite input)
+    int nb1, nb2, reserved0;            // refinement sub-bins per direction
+    int res[kFrameGrid];
+    int stride[kFrameGrid];
+    float lo[kFrameGrid];
+    float h, inv_h, margin, slack;
+    float rlo0, rlo1, rinv0, rinv1;
+    float sigma[FRNN_FRAME_DIRS];
+    int reserved1[2];
     int coord[kMaxTerms];
     float mean[kMaxTerms];
-    float w0[kMaxTerms], w1[kMaxTerms];
+    float dir[FRNN_FRAME_DIRS][kMaxTerms];
 };
-static_assert(sizeof(RefineInfo) == sizeof(frnn_refine_info_t), "RefineInfo mirrors frnn_refine_info_t");
+static_assert(sizeof(Frame) == sizeof(frnn_frame_t), "Frame mirrors frnn_frame_t");
 
-struct RefineLayout {
-    size_t info, bidx, subcnt, substart, scanpart, cov, subkey, total;   // byte offsets
+struct FrameLayout {
+    size_t frame, bidx, subcnt, substart, scanpart, cov, subkey, total;   // byte offsets
     int max_big;        // upper bound on cells with >= kBigCell points
     int nsub;           // max_big * kSubBins + 1 scanned entries
 };
 
 // Per-coordinate statistics of the input (fp64 accumulation): the mean is the
-// centre of the MFMA filter rows, variance and range choose and scale the
-// refinement axes.
+// centre of the MFMA filter rows and of the projections, variance and range
+// choose and bound the projection terms.
 struct DimStat { float mean, var, lo, hi; };
 struct StatsLayout { size_t dims, part, total; };
 StatsLayout stats_layout(int D);
 int launch_point_stats(const float* pts, int N, int D, void* stats_ws, hipStream_t s);
 
-// Number of refinement axes the plan allows (0 for brute force and full-D grids).
-inline int refine_axes(const frnn_plan_t& p, int D) {
-    if (p.path != FRNN_PATH_GRID_FIRST) return 0;
-    const int extra = D - p.grid_dim;
-    return extra <= 0 ? 0 : (extra >= 2 ? 2 : 1);
+inline bool has_frame(const frnn_plan_t& p, int D) { return p.path == FRNN_PATH_GRID_FIRST && D > p.grid_dim; }
+// Cells (count array length - 1) of a grid plan: res^g, or the frame's
+// capacity (at least res^g, which its raw-coordinate fallback uses).
+inline long long grid_cells(int N, int D, const frnn_plan_t& p) {
+    if (has_frame(p, D)) {
+        long long c = N < 4096 ? 4096 : N;
+        c = c < FRNN_MAX_CELLS ? c : FRNN_MAX_CELLS;
+        return c > p.cells ? c : p.cells;
+    }
+    return p.cells;
 }
-RefineLayout refine_layout(int N, int D, long long cells);
-int launch_refine(const float* pts, int N, int D, int g, long long cells, const int* cell_of, const int* cnt,
-                  int* rank, const void* stats_ws, void* ws, hipStream_t s);
+FrameLayout frame_layout(int N, int D, long long cells);
+// Frame of a first-coordinate plan: terms, sampled covariance, principal
+// directions, grid and sub-bin geometry.  Needs the point statistics.
+int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long long cells,
+                 const void* stats_ws, void* ws, hipStream_t s);
+// Sub-bin counting of big cells (after the scan).
+int launch_refine(const float* pts, int N, int D, long long cells, const int* cell_of, const int* cnt,
+                  int* rank, void* ws, hipStream_t s);
 
 // Launchers return 0, 1 (bad argument), 2 (size limit) or 3 (HIP launch error;
 // the error code is kept for last_launch_error()).
@@ -78,22 +93,26 @@ int launch_result();
 hipError_t last_launch_error();
 
 int launch_fill_i32(int* p, long long n, int v, hipStream_t s);
-int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, int* cell_of, int* rank,
-                     int* cnt, hipStream_t s);
+// frame_ws: bin on the frame's grid directions (first-coordinate plans; cell
+// ids are kept below `cells`, the count array's length - 1); nullptr: raw
+// coordinates
+int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, const void* frame_ws,
+                     int cells, int* cell_of, int* rank, int* cnt, hipStream_t s);
 // flag_min > 0 scans (in[i] >= flag_min) instead of in[i]
 int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s, int flag_min = 0);
-// refine_ws: workspace of launch_refine, or nullptr when the plan has no refinement.
+// frame_ws: the frame workspace (refined big cells), or nullptr.
 // stats_ws/frows/fnorm: when given, also write the centred filter rows
 // fl(x - mean) (stride aos_stride(D)) and their squared norms.
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,
-                   const int* cnt, const void* refine_ws, long long cells, int* sorted_idx, int* inv,
+                   const int* cnt, const void* frame_ws, long long cells, int* sorted_idx, int* inv,
                    float* aos, const void* stats_ws, float* frows, float* fnorm, hipStream_t s);
 int launch_transpose(const float* pts, int N, int D, float* aos, const void* stats_ws, float* frows,
                      float* fnorm, hipStream_t s);
 int launch_unpermute(const unsigned long long* lists, int cap, const int* inv, int N, int K, int* idxs,
                      float* dists, hipStream_t s);
 int launch_search(const float* aos, const float* frows, const float* fnorm, const int* sorted_idx,
-                  const int* start, const void* refine_ws, int N, int D, int K, const frnn_plan_t& plan,
-                  unsigned long long* lists, int cap, unsigned long long* counters, hipStream_t s);
+                  const int* cell_of, const int* start, const void* frame_ws, int N, int D, int K,
+                  const frnn_plan_t& plan, unsigned long long* lists, int cap, unsigned long long* counters,
+                  hipStream_t s);
 
 }  // namespace frnn

@@ -64,15 +64,17 @@ struct SearchArgs {
     const float* frows;          // the same rows centred on the input mean: fl(x - mean)
     const float* fnorm;          // squared norms of the centred rows
     const int* sorted_idx;       // sorted position -> original index (grid paths)
+    const int* cell_of;          // original index -> cell id (grid paths)
     const int* start;            // cells+1 exclusive cell offsets (grid paths)
-    const RefineInfo* ref;       // within-cell refinement, or nullptr
+    const Frame* frame;          // first-coordinate grid frame, or nullptr (raw grid)
     const int* bidx;             // big-cell index (exclusive scan of big flags)
     const int* substart;         // sub-bin offsets of big cells
     unsigned long long* lists;   // [N][cap] candidate keys
     unsigned long long* counters;
-    int N, K, cap, G, res;
+    int N, K, cap, G, res;       // res: raw-grid cells per axis
+    int gstride[kMaxG];          // raw-grid cell-id stride per axis
     int room;                    // usable list entries: min(cap, largest register sort)
-    float r2, cell, inv_cell, radius;
+    float r2, cell, radius;      // cell: raw-grid cell edge
     float norm_scale;            // 1 - c_norm
     float thr_rel, thr_abs;      // filter threshold margin
     int nchunks;
@@ -80,28 +82,6 @@ struct SearchArgs {
 
 __device__ __forceinline__ float filter_threshold(float thr, const SearchArgs& a) {
     return fmaf(thr, a.thr_rel, thr) + a.thr_abs;
-}
-
-// Lower bound of |q - x| over points x binned into cell c of one axis.  The
-// 2^-21 relative shrink covers the rounding of the binning product, of c*cell
-// and of the subtraction; edge cells are unbounded outward because binning
-// clamps.
-__device__ __forceinline__ float axis_gap(float q, int c, int res, float cell) {
-    const float eps = 4.76837158203125e-07f;
-    float g = 0.0f;
-    if (c > 0) {
-        const float lo = (float)c * cell;
-        float t = lo - q;
-        t -= eps * (fabsf(lo) + fabsf(q));
-        g = fmaxf(g, t);
-    }
-    if (c < res - 1) {
-        const float hi = (float)(c + 1) * cell;
-        float t = q - hi;
-        t -= eps * (fabsf(hi) + fabsf(q));
-        g = fmaxf(g, t);
-    }
-    return g;
 }
 
 // Exact fp32 squared distance in the reference's order: sequential
@@ -166,8 +146,13 @@ void search_kernel(SearchArgs a) {
     __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing], r_x[kRing], r_seg[kRing];
     // current tile: candidate row -> sorted position, cell x, segment id
     __shared__ int t_pos[32], t_x[32], t_seg[32];
+    // grid geometry per axis (cells, cell-id stride, origin), the segment's
+    // bounding box and row coordinates, and each query's grid coordinates
+    __shared__ int s_res[kMaxG], s_stride[kMaxG];
+    __shared__ float s_org[kMaxG];
     __shared__ float s_blo[kMaxG], s_bhi[kMaxG];
     __shared__ int s_rc[kMaxG];
+    __shared__ float s_qg[BF ? 1 : kQB * kMaxG];
 
     const int lane = threadIdx.x;
     const int n = lane & 31;
@@ -541,25 +526,73 @@ void search_kernel(SearchArgs a) {
         append_runs(0, lane == 0 ? a.N : 0, 0, 0);
         consume(true);
     } else {
-        const float* qrow = query_row(qvalid ? n : 0);
-        x_n = bin_coord(qrow[0], a.inv_cell, a.res);
-        int row_n = 0;
-        {
-            int mul = 1;
-            for (int d = 1; d < a.G; ++d) {
-                row_n += bin_coord(qrow[d], a.inv_cell, a.res) * mul;
-                mul *= a.res;
-            }
+        // Grid geometry: the frame's projected axes (first-coordinate plans)
+        // or the raw coordinates on the plan's cells.  Cell ci of axis d spans
+        // [org_d + ci h, org_d + (ci + 1) h]; the binned values of its points
+        // lie within slack of that span (edge cells are unbounded outward, as
+        // binning clamps) and within margin of the exact projections, so the
+        // per-axis gaps below shrink by slack + 2 margin (0 on raw grids).
+        // Frame directions have norm < 1 and are orthonormal up to a shrink,
+        // so the gaps lower-bound the distance.
+        const Frame* fr = a.frame;
+        const bool proj = fr != nullptr && fr->projected != 0;
+        const int G = a.G;
+        const int res0 = fr ? fr->res[0] : a.res;
+        const float gh = fr ? fr->h : a.cell;
+        const float gsm = fr ? fr->slack + 2.0f * fr->margin : 0.0f;
+        const int L = fr ? fr->L : 0;
+        if (lane < G) {
+            s_res[lane] = fr ? fr->res[lane] : a.res;
+            s_stride[lane] = fr ? fr->stride[lane] : a.gstride[lane];
+            s_org[lane] = fr ? fr->lo[lane] : 0.0f;
         }
-        if (!qvalid) row_n = 0x7fffffff;
+        // this lane's query: grid coordinates (projections or raw values) and
+        // its projections onto the refinement directions
+        const float* qrow = query_row(qvalid ? n : 0);
+        float pj0 = 0.0f, pj1 = 0.0f;
+        if (proj) {
+            float sp[FRNN_FRAME_DIRS];
+            frame_project(fr, 0, [&](int d) { return qrow[d]; }, sp);
+            if (h == 0) {
+#pragma unroll
+                for (int d = 0; d < kFrameGrid; ++d)
+                    if (d < G) s_qg[n * kMaxG + d] = sp[d];
+            }
+            pj0 = sp[kRefDir0];
+            pj1 = sp[kRefDir0 + 1];
+        } else if (h == 0) {
+            for (int d = 0; d < G; ++d) s_qg[n * kMaxG + d] = qrow[d];
+        }
+        // the query's cell, as binned: x along axis 0, the row as the id of
+        // the row's x = 0 cell (rows are non-decreasing in the sorted order)
+        int row_n = 0x7fffffff;
+        if (qvalid) {
+            const int c = a.cell_of[a.sorted_idx[q0 + n]];
+            x_n = c % res0;
+            row_n = c - x_n;
+        }
+        lds_sync();
         int nrows = 1;
-        for (int d = 1; d < a.G; ++d) nrows *= 3;
+        for (int d = 1; d < G; ++d) nrows *= 3;
         const float keep = 0.9999847412109375f;   // 1 - 2^-16
         const float eps = 4.76837158203125e-07f;  // 2^-21
-        const int L = a.ref ? a.ref->L : 0;
-        // this lane's query projected onto the refinement directions
-        float pj0 = 0.0f, pj1 = 0.0f;
-        if (L > 0) refine_project(a.ref, [&](int d) { return qrow[d]; }, pj0, pj1);
+        // lower bound of the distance along axis d from the segment's box to
+        // cell ci
+        auto axis_gap = [&](int d, int ci) __attribute__((always_inline)) -> float {
+            float gap = 0.0f;
+            const float org = s_org[d];
+            if (ci > 0) {
+                const float lo = fmaf((float)ci, gh, org);
+                const float bh = s_bhi[d];
+                gap = fmaxf(gap, (lo - bh) - eps * (fabsf(lo) + fabsf(bh)));
+            }
+            if (ci < s_res[d] - 1) {
+                const float hi = fmaf((float)(ci + 1), gh, org);
+                const float bl = s_blo[d];
+                gap = fmaxf(gap, (bl - hi) - eps * (fabsf(hi) + fabsf(bl)));
+            }
+            return fmaxf(gap - gsm, 0.0f);
+        };
 
         // One loop walks the segments (runs of queries sharing a row) and, per
         // segment, batches of 64 traversal items; every iteration appends at
@@ -582,16 +615,16 @@ void search_kernel(SearchArgs a) {
                 // non-decreasing in the cell-sorted order); at least one step,
                 // so every wave terminates even on unsorted input
                 seg = max(seg + 1, (int)__popcll(__ballot(row_n <= R) & 0xffffffffull));
-                // segment bounding box on the gridded axes and the largest threshold
-                for (int d = 0; d < a.G; ++d) {
-                    const float qd = qrow[d];
+                // segment bounding box on the grid axes and the largest threshold
+                for (int d = 0; d < G; ++d) {
+                    const float qd = s_qg[n * kMaxG + d];
                     const float lo = wave_min_f32(in_seg ? qd : __builtin_huge_valf());
                     const float hi = wave_max_f32(in_seg ? qd : -__builtin_huge_valf());
-                    if (lane == 0) { s_blo[d] = lo; s_bhi[d] = hi; }
-                }
-                if (lane == 0) {
-                    int Rt = R;
-                    for (int d = 1; d < a.G; ++d) { s_rc[d] = Rt % a.res; Rt /= a.res; }
+                    if (lane == 0) {
+                        s_blo[d] = lo;
+                        s_bhi[d] = hi;
+                        s_rc[d] = d > 0 ? (R / s_stride[d]) % s_res[d] : 0;
+                    }
                 }
                 thr_seg = wave_max_f32(in_seg ? key_d2(s_thr[n]) : -__builtin_huge_valf());
                 // refinement windows: a candidate within the radius of a segment
@@ -604,43 +637,40 @@ void search_kernel(SearchArgs a) {
                 qlo0 = qlo1 = qhi1 = 0;
                 nb2 = 1;
                 if (L > 0) {
-                    const RefineInfo* rf = a.ref;
-                    nb2 = rf->nb2;
-                    const float hw = a.radius * 1.000030517578125f + 2.0f * rf->margin;
+                    nb2 = fr->nb2;
+                    const float hw = a.radius * 1.000030517578125f + 2.0f * fr->margin;
                     const float lo0 = wave_min_f32(in_seg ? pj0 : __builtin_huge_valf());
                     const float hi0 = wave_max_f32(in_seg ? pj0 : -__builtin_huge_valf());
                     const float h0 = hw + 2.384185791015625e-07f * (fabsf(lo0) + fabsf(hi0));
-                    qlo0 = sub_bin(lo0 - h0, rf->lo0, rf->inv0, rf->nb1);
-                    qhi0 = sub_bin(hi0 + h0, rf->lo0, rf->inv0, rf->nb1);
+                    qlo0 = sub_bin(lo0 - h0, fr->rlo0, fr->rinv0, fr->nb1);
+                    qhi0 = sub_bin(hi0 + h0, fr->rlo0, fr->rinv0, fr->nb1);
                     if (L > 1) {
                         const float lo1 = wave_min_f32(in_seg ? pj1 : __builtin_huge_valf());
                         const float hi1 = wave_max_f32(in_seg ? pj1 : -__builtin_huge_valf());
                         const float h1 = hw + 2.384185791015625e-07f * (fabsf(lo1) + fabsf(hi1));
-                        qlo1 = sub_bin(lo1 - h1, rf->lo1, rf->inv1, rf->nb2);
-                        qhi1 = sub_bin(hi1 + h1, rf->lo1, rf->inv1, rf->nb2);
+                        qlo1 = sub_bin(lo1 - h1, fr->rlo1, fr->rinv1, fr->nb2);
+                        qhi1 = sub_bin(hi1 + h1, fr->rlo1, fr->rinv1, fr->nb2);
                     }
                 }
                 lds_sync();
 
                 if (a.counters && in_seg && h == 0) {
                     for (int t = 0; t < nrows; ++t) {
-                        int tt = t, Rn = 0, mul = 1;
+                        int tt = t, Rb = 0;
                         bool ok = true;
-                        for (int d = 1; d < a.G; ++d) {
+                        for (int d = 1; d < G; ++d) {
                             const int cc = s_rc[d] + (tt % 3) - 1;
                             tt /= 3;
-                            ok = ok && cc >= 0 && cc < a.res;
-                            Rn += cc * mul;
-                            mul *= a.res;
+                            ok = ok && cc >= 0 && cc < s_res[d];
+                            Rb += cc * s_stride[d];
                         }
                         if (!ok) continue;
-                        const int base = Rn * a.res;
-                        c_shell += a.start[base + min(x_n + 1, a.res - 1) + 1] - a.start[base + max(x_n - 1, 0)];
+                        c_shell += a.start[Rb + min(x_n + 1, res0 - 1) + 1] - a.start[Rb + max(x_n - 1, 0)];
                     }
                 }
 
                 xa = max(xlo - 1, 0);
-                nx = min(xhi + 1, a.res - 1) - xa + 1;
+                nx = min(xhi + 1, res0 - 1) - xa + 1;
                 nq1 = L > 0 ? max(qhi0 - qlo0 + 1, 0) : 1;
                 NI = nx * nrows * nq1;
                 ib = 0;
@@ -652,52 +682,43 @@ void search_kernel(SearchArgs a) {
                     const int q1i = item % nq1;
                     const int rest = item / nq1;
                     const int x = xa + rest % nx;
-                    int tt = rest / nx, Rn = 0, mul = 1;
+                    int tt = rest / nx, Rb = 0;
                     bool ok = true;
-                    for (int d = 1; d < a.G; ++d) {
+                    // conservative AABB test of the whole cell against the
+                    // segment's queries
+                    float lb = 0.0f;
+                    {
+                        const float gp = axis_gap(0, x);
+                        lb = gp * gp;
+                    }
+                    for (int d = 1; d < G; ++d) {
                         const int cc = s_rc[d] + (tt % 3) - 1;
                         tt /= 3;
-                        ok = ok && cc >= 0 && cc < a.res;
-                        Rn += cc * mul;
-                        mul *= a.res;
+                        const bool in = cc >= 0 && cc < s_res[d];
+                        ok = ok && in;
+                        Rb += cc * s_stride[d];
+                        if (in) {
+                            const float gp = axis_gap(d, cc);
+                            lb = fmaf(gp, gp, lb);
+                        }
                     }
                     rxv = x;
                     if (ok) {
-                        const int c = x + a.res * Rn;
+                        const int c = x + Rb;
                         const int cs = a.start[c];
                         const int ce = a.start[c + 1];
-                        if (ce > cs) {
-                            // conservative AABB test of the whole cell against the
-                            // segment's queries
-                            float lb = 0.0f;
-                            int cd = c;
-                            for (int d = 0; d < a.G; ++d) {
-                                const int ci = cd % a.res;
-                                cd /= a.res;
-                                float gap = 0.0f;
-                                if (ci > 0) {
-                                    const float lo = (float)ci * a.cell;
-                                    gap = fmaxf(gap, (lo - s_bhi[d]) - eps * (fabsf(lo) + fabsf(s_bhi[d])));
-                                }
-                                if (ci < a.res - 1) {
-                                    const float hi = (float)(ci + 1) * a.cell;
-                                    gap = fmaxf(gap, (s_blo[d] - hi) - eps * (fabsf(hi) + fabsf(s_blo[d])));
-                                }
-                                lb = fmaf(gap, gap, lb);
-                            }
-                            if (!(lb * keep > thr_seg)) {
-                                if (L > 0 && ce - cs >= kBigCell) {
-                                    const int q1 = qlo0 + q1i;
-                                    const size_t sb = (size_t)a.bidx[c] * kSubBins;
-                                    const int s0 = a.substart[sb];
-                                    const int sl = a.substart[sb + q1 * nb2 + qlo1];
-                                    const int sh = a.substart[sb + q1 * nb2 + qhi1 + 1];
-                                    rs = cs + (sl - s0);
-                                    rl = sh - sl;
-                                } else if (q1i == 0) {
-                                    rs = cs;
-                                    rl = ce - cs;
-                                }
+                        if (ce > cs && !(lb * keep > thr_seg)) {
+                            if (L > 0 && ce - cs >= kBigCell) {
+                                const int q1 = qlo0 + q1i;
+                                const size_t sb = (size_t)a.bidx[c] * kSubBins;
+                                const int s0 = a.substart[sb];
+                                const int sl = a.substart[sb + q1 * nb2 + qlo1];
+                                const int sh = a.substart[sb + q1 * nb2 + qhi1 + 1];
+                                rs = cs + (sl - s0);
+                                rl = sh - sl;
+                            } else if (q1i == 0) {
+                                rs = cs;
+                                rl = ce - cs;
                             }
                         }
                     }
@@ -747,17 +768,20 @@ static void launch_ds(const SearchArgs& a, bool bf, hipStream_t s) {
 }
 
 int launch_search(const float* aos, const float* frows, const float* fnorm, const int* sorted_idx,
-                  const int* start, const void* refine_ws, int N, int D, int K, const frnn_plan_t& plan,
-                  unsigned long long* lists, int cap, unsigned long long* counters, hipStream_t s) {
+                  const int* cell_of, const int* start, const void* frame_ws, int N, int D, int K,
+                  const frnn_plan_t& plan, unsigned long long* lists, int cap, unsigned long long* counters,
+                  hipStream_t s) {
     if (N <= 0) return 0;
     const bool bf = plan.path == FRNN_PATH_BRUTEFORCE;
-    if (!bf && (plan.grid_dim < 1 || plan.grid_dim > 9)) return 1;
+    if (!bf && (plan.grid_dim < 1 || plan.grid_dim > kMaxG || !sorted_idx || !cell_of || !start)) return 1;
+    if (!bf && frame_ws && plan.grid_dim > kFrameGrid) return 1;
     if (cap < list_capacity(K) || K > FRNN_MAX_K || !frows || !fnorm) return 1;
     SearchArgs a{};
     a.pts = aos;
     a.frows = frows;
     a.fnorm = fnorm;
     a.sorted_idx = sorted_idx;
+    a.cell_of = cell_of;
     a.start = start;
     a.lists = lists;
     a.counters = counters;
@@ -767,15 +791,22 @@ int launch_search(const float* aos, const float* frows, const float* fnorm, cons
     a.room = min(cap, 4 * kWave);
     a.G = bf ? 0 : plan.grid_dim;
     a.res = bf ? 1 : plan.res;
+    {
+        long long st = 1;
+        for (int d = 0; d < kMaxG; ++d) {
+            a.gstride[d] = (int)st;
+            if (d < a.G) st *= a.res;
+            if (st > FRNN_MAX_CELLS) st = FRNN_MAX_CELLS;
+        }
+    }
     a.r2 = plan.r2;
-    a.inv_cell = plan.inv_cell;
     const int DS = aos_stride(D);
     a.cell = bf ? 1.0f : plan.cell_size;
     a.radius = plan.cell_size;
-    if (refine_ws && !bf) {
-        const RefineLayout L = refine_layout(N, D, plan.cells);
-        const char* base = static_cast<const char*>(refine_ws);
-        a.ref = reinterpret_cast<const RefineInfo*>(base + L.info);
+    if (frame_ws && !bf) {
+        const FrameLayout L = frame_layout(N, D, grid_cells(N, D, plan));
+        const char* base = static_cast<const char*>(frame_ws);
+        a.frame = reinterpret_cast<const Frame*>(base + L.frame);
         a.bidx = reinterpret_cast<const int*>(base + L.bidx);
         a.substart = reinterpret_cast<const int*>(base + L.substart);
     }

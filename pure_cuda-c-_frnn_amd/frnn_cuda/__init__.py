@@ -24,9 +24,10 @@ __all__ = ["FRNNEngine", "plan", "FRNNError", "LIB_PATH", "MAX_K", "MAX_DIM", "M
 MAX_K = 128
 MAX_DIM = 128
 MAX_CELLS = 1_000_000
-NUM_STAGES = 8
+NUM_STAGES = 9
 NUM_COUNTERS = 4
-STAGE_NAMES = ("zero_fill", "bin_count", "stats", "scan", "refine", "reorder", "search", "unpermute")
+STAGE_NAMES = ("zero_fill", "stats", "frame", "bin_count", "scan", "refine", "reorder", "search",
+               "unpermute")
 PATH_NAMES = {-1: "empty", 0: "bruteforce", 1: "grid_full", 2: "grid_first"}
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -50,22 +51,34 @@ class _Plan(ctypes.Structure):
                 "r2": self.r2, "cell_size": self.cell_size, "inv_cell": self.inv_cell}
 
 
-REFINE_TERMS = 32
+FRAME_TERMS = 32
+FRAME_DIRS = 6
+FRAME_GRID = 4
 
 
-class RefineInfo(ctypes.Structure):
-    """frnn_refine_info_t: the descriptor at the start of a refinement workspace."""
-    _fields_ = [("axes", ctypes.c_int), ("bins0", ctypes.c_int), ("bins1", ctypes.c_int),
-                ("terms", ctypes.c_int), ("lo0", ctypes.c_float), ("lo1", ctypes.c_float),
-                ("inv0", ctypes.c_float), ("inv1", ctypes.c_float), ("margin", ctypes.c_float),
-                ("reserved", ctypes.c_int * 7), ("coord", ctypes.c_int * REFINE_TERMS),
-                ("mean", ctypes.c_float * REFINE_TERMS), ("w0", ctypes.c_float * REFINE_TERMS),
-                ("w1", ctypes.c_float * REFINE_TERMS)]
+class FrameInfo(ctypes.Structure):
+    """frnn_frame_t: the descriptor at the start of a frame workspace."""
+    _fields_ = [("grid_dim", ctypes.c_int), ("cells", ctypes.c_int), ("terms", ctypes.c_int),
+                ("axes", ctypes.c_int), ("projected", ctypes.c_int), ("bins0", ctypes.c_int),
+                ("bins1", ctypes.c_int), ("reserved0", ctypes.c_int),
+                ("res", ctypes.c_int * FRAME_GRID), ("stride", ctypes.c_int * FRAME_GRID),
+                ("lo", ctypes.c_float * FRAME_GRID), ("h", ctypes.c_float), ("inv_h", ctypes.c_float),
+                ("margin", ctypes.c_float), ("slack", ctypes.c_float),
+                ("rlo0", ctypes.c_float), ("rlo1", ctypes.c_float),
+                ("rinv0", ctypes.c_float), ("rinv1", ctypes.c_float),
+                ("sigma", ctypes.c_float * FRAME_DIRS), ("reserved1", ctypes.c_int * 2),
+                ("coord", ctypes.c_int * FRAME_TERMS), ("mean", ctypes.c_float * FRAME_TERMS),
+                ("dir", (ctypes.c_float * FRAME_TERMS) * FRAME_DIRS)]
 
     @classmethod
     def from_workspace(cls, head):
-        """Decode from the first bytes of a refinement workspace (bytes or uint8 array)."""
+        """Decode from the first bytes of a frame workspace (bytes or uint8 array)."""
         return cls.from_buffer_copy(bytes(np.asarray(head, dtype=np.uint8)[:ctypes.sizeof(cls)]))
+
+    def directions(self):
+        """(6, 32) float32 array of direction weights over the term coordinates."""
+        return np.array([[self.dir[k][t] for t in range(FRAME_TERMS)] for k in range(FRAME_DIRS)],
+                        dtype=np.float32)
 
 
 _lib = None
@@ -102,16 +115,18 @@ def _load():
         "frnn_engine_set_profiling": ([vp, i32], i32),
         "frnn_engine_stage_times": ([vp, vp, i32], i32),
         "frnn_engine_counters": ([vp, vp, i32], i32),
-        "frnn_launch_bin_count": ([vp, i32, i32, i32, f32, i64, vp, vp, vp, vp], i32),
+        "frnn_grid_cells": ([i32, i32, ctypes.POINTER(_Plan)], i64),
+        "frnn_launch_bin_count": ([vp, i32, i32, i32, f32, i64, vp, vp, vp, vp, vp], i32),
         "frnn_launch_exclusive_scan": ([vp, i32, vp, vp, vp], i32),
         "frnn_stats_workspace_bytes": ([i32], i64),
         "frnn_launch_point_stats": ([vp, i32, i32, vp, vp], i32),
-        "frnn_refine_workspace_bytes": ([i32, i32, ctypes.POINTER(_Plan)], i64),
-        "frnn_launch_refine": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp, vp, vp, vp], i32),
+        "frnn_frame_workspace_bytes": ([i32, i32, ctypes.POINTER(_Plan)], i64),
+        "frnn_launch_frame": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp], i32),
+        "frnn_launch_refine": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp, vp, vp], i32),
         "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, vp], i32),
         "frnn_launch_transpose": ([vp, i32, i32, vp, vp, vp, vp, vp], i32),
-        "frnn_launch_find_nbrs": ([vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan), vp,
-                                   i32, vp, vp], i32),
+        "frnn_launch_find_nbrs": ([vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan),
+                                   vp, i32, vp, vp], i32),
         "frnn_launch_unpermute": ([vp, i32, vp, i32, i32, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
@@ -144,10 +159,15 @@ def _plan_struct(N, dim, K, radius):
     return p
 
 
-def refine_workspace_bytes(N, dim, K, radius):
-    """Bytes of the within-cell refinement workspace for this problem (0: none)."""
-    return int(_load().frnn_refine_workspace_bytes(int(N), int(dim),
-                                                   ctypes.byref(_plan_struct(N, dim, K, radius))))
+def frame_workspace_bytes(N, dim, K, radius):
+    """Bytes of the grid-frame workspace for this problem (0: the plan has no frame)."""
+    return int(_load().frnn_frame_workspace_bytes(int(N), int(dim),
+                                                  ctypes.byref(_plan_struct(N, dim, K, radius))))
+
+
+def grid_cells(N, dim, K, radius):
+    """Cells of the problem's grid (count arrays hold one more); 0 for brute force."""
+    return int(_load().frnn_grid_cells(int(N), int(dim), ctypes.byref(_plan_struct(N, dim, K, radius))))
 
 
 def aos_stride(dim):

@@ -96,29 +96,50 @@ def test_status_strings():
 def test_launch_seam_rejects_bad_geometry_without_touching_the_device():
     L = frnn_cuda._load()
     # cells != res^g, grid_dim out of range, null pointers: all rejected on the host
-    assert L.frnn_launch_bin_count(None, 10, 2, 4, 1.0, 15, None, None, None, None) == 1
-    assert L.frnn_launch_bin_count(None, 10, 0, 4, 1.0, 1, None, None, None, None) == 1
-    assert L.frnn_launch_bin_count(None, 10, 2, 4, 1.0, 16, None, None, None, None) == 1
+    assert L.frnn_launch_bin_count(None, 10, 2, 4, 1.0, 15, None, None, None, None, None) == 1
+    assert L.frnn_launch_bin_count(None, 10, 0, 4, 1.0, 1, None, None, None, None, None) == 1
+    assert L.frnn_launch_bin_count(None, 10, 2, 4, 1.0, 16, None, None, None, None, None) == 1
+    # a frame grid has at most 4 axes and a cell count within the cap
+    ws = ctypes.c_void_p(1)
+    assert L.frnn_launch_bin_count(None, 10, 5, 4, 1.0, 100, ws, None, None, None, None) == 1
+    assert L.frnn_launch_bin_count(None, 10, 4, 4, 1.0, 1_000_001, ws, None, None, None, None) == 1
     assert L.frnn_launch_exclusive_scan(None, 5, None, None, None) == 1
     assert L.frnn_launch_unpermute(None, 10, None, 5, 20, None, None, None) == 1
     p = frnn_cuda._Plan()
     assert L.frnn_make_plan(100000, 12, 32, ctypes.c_float(0.0345), ctypes.byref(p)) == 0
+    assert L.frnn_launch_frame(None, 10, 12, ctypes.byref(p), None, None, None) == 1   # null pointers
+    assert L.frnn_launch_refine(None, 10, 12, ctypes.byref(p), None, None, None, None, None) == 1
     p.cells = 5
-    assert L.frnn_launch_find_nbrs(None, None, None, None, None, None, 100000, 12, 32, ctypes.byref(p),
+    assert L.frnn_launch_find_nbrs(None, None, None, None, None, None, None, 100000, 12, 32, ctypes.byref(p),
                                    None, 128, None, None) == 1
-    assert L.frnn_launch_refine(None, 10, 12, None, None, None, None, None, None, None) == 1
+    assert L.frnn_launch_frame(None, 10, 12, ctypes.byref(p), None, None, None) == 1   # inconsistent plan
+    assert L.frnn_launch_refine(None, 10, 12, None, None, None, None, None, None) == 1
+    q = frnn_cuda._Plan()
+    assert L.frnn_make_plan(100000, 3, 16, ctypes.c_float(0.1), ctypes.byref(q)) == 0
+    assert L.frnn_launch_frame(None, 10, 3, ctypes.byref(q), None, None, None) == 1     # no frame
     assert L.frnn_launch_reorder(None, 10, 3, None, None, None, None, None, 0, None, None, None, None, None,
                                  None, None) == 1
     assert L.frnn_launch_point_stats(None, 10, 3, None, None) == 1
     assert L.frnn_stats_workspace_bytes(0) == -1 and L.frnn_stats_workspace_bytes(16) > 0
 
 
-def test_refine_workspace_sizes():
-    # refinement only for first-coordinate plans with dim > grid_dim
-    assert frnn_cuda.refine_workspace_bytes(100000, 12, 32, 0.0345) > 0     # grid_first g=4
-    assert frnn_cuda.refine_workspace_bytes(100000, 3, 16, 0.1) == 0        # full-D grid
-    assert frnn_cuda.refine_workspace_bytes(200000, 128, 128, 12.96) == 0   # brute force
-    assert frnn_cuda.refine_workspace_bytes(100000, 4, 8, 0.02) > 0         # grid_first g=3, one axis
+def test_frame_workspace_sizes():
+    # a frame only for first-coordinate plans with dim > grid_dim
+    assert frnn_cuda.frame_workspace_bytes(100000, 12, 32, 0.0345) > 0     # grid_first g=4
+    assert frnn_cuda.frame_workspace_bytes(100000, 3, 16, 0.1) == 0        # full-D grid
+    assert frnn_cuda.frame_workspace_bytes(200000, 128, 128, 12.96) == 0   # brute force
+    assert frnn_cuda.frame_workspace_bytes(100000, 4, 8, 0.02) > 0         # grid_first g=3
+
+
+def test_grid_cells():
+    # raw grids use res^g; a frame's capacity is clamp(N, 4096, 1M), at least res^g
+    p = frnn_cuda.plan(100000, 3, 16, 0.1)
+    assert frnn_cuda.grid_cells(100000, 3, 16, 0.1) == p["cells"]
+    assert frnn_cuda.grid_cells(200000, 128, 128, 12.96) == 0
+    assert frnn_cuda.grid_cells(100000, 12, 32, 0.0345) == max(100000, frnn_cuda.plan(100000, 12, 32, 0.0345)["cells"])
+    assert frnn_cuda.grid_cells(100000, 12, 32, 0.2) == 100000
+    assert frnn_cuda.grid_cells(1000, 12, 32, 0.0345) == max(4096, frnn_cuda.plan(1000, 12, 32, 0.0345)["cells"])
+    assert frnn_cuda.grid_cells(3_000_000, 12, 32, 0.0345) == 1_000_000
 
 
 @pytest.mark.skipif(gpu_visible(), reason="checks the no-device error path")
@@ -130,3 +151,19 @@ def test_engine_without_device_raises():
 def test_engine_rejects_bad_max_points():
     with pytest.raises(ValueError):
         frnn_cuda.FRNNEngine(max_points=0)
+
+
+def test_frame_struct_layout_matches_header(tmp_path):
+    # the ctypes mirror of frnn_frame_t against the C compiler's layout
+    src = tmp_path / "frame_layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "frnn_mi355x.h"\n'
+                   'int main(void) { printf("%zu %zu %zu %zu %zu", sizeof(frnn_frame_t), '
+                   'offsetof(frnn_frame_t, h), offsetof(frnn_frame_t, sigma), '
+                   'offsetof(frnn_frame_t, coord), offsetof(frnn_frame_t, dir)); return 0; }\n')
+    exe = tmp_path / "frame_layout"
+    import subprocess
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    F = frnn_cuda.FrameInfo
+    assert got == [ctypes.sizeof(F), F.h.offset, F.sigma.offset, F.coord.offset, F.dir.offset]

@@ -3,6 +3,8 @@
 bin/count  vs the oracle's clamped binning and numpy bincount
 scan       vs numpy cumsum (exclusive)
 reorder    permutation / cell-order / row-copy invariants
+frame      descriptor, binning recomputed in exact fp32, the 3^g shell
+           guarantee on sampled pairs, sub-bin order inside big cells
 """
 import ctypes
 
@@ -27,8 +29,8 @@ def _build(X, g, res, inv):
     cell_of = t.empty(N, dtype=t.int32, device="cuda:0")
     rank = t.empty(N, dtype=t.int32, device="cuda:0")
     cnt = t.full((cells + 1,), -7, dtype=t.int32, device="cuda:0")
-    rc = L.frnn_launch_bin_count(vp(d), N, g, res, ctypes.c_float(inv), cells, vp(cell_of), vp(rank),
-                                 vp(cnt), None)
+    rc = L.frnn_launch_bin_count(vp(d), N, g, res, ctypes.c_float(inv), cells, None, vp(cell_of),
+                                 vp(rank), vp(cnt), None)
     assert rc == 0
     start = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
     part = t.empty(frnn_cuda.scan_partials_count(cells + 1), dtype=t.int32, device="cuda:0")
@@ -116,126 +118,185 @@ def _sub_bins(x, lo, inv, nb):
     return f.astype(np.int64)
 
 
-def _project(X, ri):
-    """The refinement projections in fp32: s = fma(w[t], fl(x[coord[t]] - mean[t]), s)."""
-    s0 = np.zeros(len(X), np.float32)
-    s1 = np.zeros(len(X), np.float32)
-    for t in range(ri.terms):
-        y = (X[:, ri.coord[t]] - np.float32(ri.mean[t])).astype(np.float32)
-        s0 = E.fma32(np.float32(ri.w0[t]), y, s0)
-        s1 = E.fma32(np.float32(ri.w1[t]), y, s1)
-    return s0, s1
+def _project(X, fi, slots):
+    """Frame projections in fp32: s = fma(dir[k][t], fl(x[coord[t]] - mean[t]), s) over the terms."""
+    out = []
+    for k in slots:
+        s = np.zeros(len(X), np.float32)
+        for t in range(fi.terms):
+            y = (X[:, fi.coord[t]] - np.float32(fi.mean[t])).astype(np.float32)
+            s = E.fma32(np.float32(fi.dir[k][t]), y, s)
+        out.append(s)
+    return out
 
 
-@pytest.mark.parametrize("name,N", [("metric", 300_000), ("C3", 300_000)])
-def test_refinement_orders_big_cells(name, N):
-    """Within-cell refinement: the projection descriptor (terms, weights, margin,
-    bin geometry), the sub-bin order inside big cells, and the usual permutation /
-    cell-order / row-copy invariants of the reorder."""
+def _frame_build(X, K, radius):
+    """stats -> frame -> bin/count -> scan -> refine -> reorder through the seam."""
     t = torch()
-    w = W.config(name, N=N)
-    plan = frnn_cuda._plan_struct(N, w.D, w.K, w.radius)
-    assert plan.path == 2 and plan.grid_dim == 4
-    g, res, cells = plan.grid_dim, plan.res, plan.cells
+    N, D = X.shape
+    plan = frnn_cuda._plan_struct(N, D, K, radius)
     L = frnn_cuda._load()
-    log(f"refinement {name} N={N} res={res}")
-    d = device_soa(w.X)
+    cells = L.frnn_grid_cells(N, D, ctypes.byref(plan))
+    d = device_soa(X)
+    sws = t.zeros(L.frnn_stats_workspace_bytes(D), dtype=t.uint8, device="cuda:0")
+    assert L.frnn_launch_point_stats(vp(d), N, D, vp(sws), None) == 0
+    wsb = L.frnn_frame_workspace_bytes(N, D, ctypes.byref(plan))
+    assert wsb > 0
+    ws = t.zeros(wsb, dtype=t.uint8, device="cuda:0")
+    assert L.frnn_launch_frame(vp(d), N, D, ctypes.byref(plan), vp(sws), vp(ws), None) == 0
     cell_of = t.empty(N, dtype=t.int32, device="cuda:0")
     rank = t.empty(N, dtype=t.int32, device="cuda:0")
     cnt = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
-    assert L.frnn_launch_bin_count(vp(d), N, g, res, ctypes.c_float(plan.inv_cell), cells, vp(cell_of),
-                                   vp(rank), vp(cnt), None) == 0
+    assert L.frnn_launch_bin_count(vp(d), N, plan.grid_dim, plan.res, ctypes.c_float(plan.inv_cell), cells,
+                                   vp(ws), vp(cell_of), vp(rank), vp(cnt), None) == 0
     start = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
     part = t.empty(frnn_cuda.scan_partials_count(cells + 1), dtype=t.int32, device="cuda:0")
     assert L.frnn_launch_exclusive_scan(vp(cnt), cells + 1, vp(start), vp(part), None) == 0
-    sws = t.zeros(L.frnn_stats_workspace_bytes(w.D), dtype=t.uint8, device="cuda:0")
-    assert L.frnn_launch_point_stats(vp(d), N, w.D, vp(sws), None) == 0
-    wsb = L.frnn_refine_workspace_bytes(N, w.D, ctypes.byref(plan))
-    assert wsb > 0
-    ws = t.zeros(wsb, dtype=t.uint8, device="cuda:0")
-    assert L.frnn_launch_refine(vp(d), N, w.D, ctypes.byref(plan), vp(cell_of), vp(cnt), vp(rank),
-                                vp(sws), vp(ws), None) == 0
-    ds = frnn_cuda.aos_stride(w.D)
+    assert L.frnn_launch_refine(vp(d), N, D, ctypes.byref(plan), vp(cell_of), vp(cnt), vp(rank), vp(ws),
+                                None) == 0
+    ds = frnn_cuda.aos_stride(D)
     sidx = t.empty(N, dtype=t.int32, device="cuda:0")
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
     frows = t.empty(N * ds, dtype=t.float32, device="cuda:0")
     fnorm = t.empty(N, dtype=t.float32, device="cuda:0")
-    assert L.frnn_launch_reorder(vp(d), N, w.D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
                                  vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), vp(fnorm), None) == 0
     t.cuda.synchronize()
-    ri = frnn_cuda.RefineInfo.from_workspace(ws[:1024].cpu().numpy())
-    stats = sws[:16 * w.D].cpu().numpy().view(np.float32).reshape(w.D, 4)
-    mean, var, lo, hi = (stats[:, k] for k in range(4))
-    T = min(w.D - g, 32)
-    assert ri.axes == 2 and ri.bins0 * ri.bins1 == 1024 and ri.terms == T
-    # terms: the highest-variance non-grid coordinates, lower index on ties
-    order = g + np.argsort(-var[g:], kind="stable")
-    coord = np.array(ri.coord[:T])
-    assert np.array_equal(coord, order[:T])
-    assert np.array_equal(np.array(ri.mean[:T], np.float32), mean[coord])
-    W0 = np.array(ri.w0[:T], np.float64)
-    W1 = np.array(ri.w1[:T], np.float64)
-    assert np.linalg.norm(W0) < 1 and np.linalg.norm(W1) < 1
-    assert abs(np.linalg.norm(W0) - 1) < 1e-5 and abs(np.linalg.norm(W1) - 1) < 1e-5 and abs(W0 @ W1) < 1e-5
-    # the directions capture (nearly) the variance of the top-2 principal
-    # subspace of the terms; the subspace itself is ill-defined when the second
-    # and third eigenvalues nearly tie (C3), and only pruning depends on it
-    Y = (w.X[:, coord] - mean[coord]).astype(np.float64)
-    C = Y.T @ Y / N
-    ev = np.linalg.eigvalsh(C)[::-1]
-    captured = W0 @ C @ W0 + W1 @ C @ W1
-    assert captured >= 0.97 * (ev[0] + ev[1]), (captured, ev[:3])
-    # bins span +-2.5 standard deviations of each projection (the library
-    # estimates the covariance from a sample of >= 128K points: 3% tolerance)
-    for wk, lok, invk, nbk in ((W0, ri.lo0, ri.inv0, ri.bins0), (W1, ri.lo1, ri.inv1, ri.bins1)):
-        sg = np.sqrt(wk @ C @ wk)
-        assert abs(lok + 2.5 * sg) <= 0.03 * 2.5 * sg and abs(invk * 5 * sg / nbk - 1) <= 0.03
-        assert lok == np.float32(lok) and abs(invk * (-2 * lok) / nbk - 1) < 1e-5
-    # margin >= (T + 2) u |x - mean| over the input
-    R = np.sqrt(np.sum(np.maximum(hi[coord].astype(np.float64) - mean[coord], mean[coord] - lo[coord].astype(np.float64)) ** 2))
-    assert ri.margin >= (T + 2) * 2.0 ** -24 * R
-    assert ri.margin <= 1.01 * (T + 2) * 2.0 ** -24 * R
-    # the window bound: pairs within the radius project within r(1 + 2^-15) + 2 margin
-    s0, s1 = _project(w.X, ri)
-    rs = np.random.RandomState(5)
-    r = float(np.float32(w.radius))
-    r2 = np.float32(np.float32(w.radius) ** 2)
-    X64 = w.X.astype(np.float64)
+    out = {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start, sidx=sidx,
+                                                 inv=inv_p, aos=aos, frows=frows, fnorm=fnorm).items()}
+    out["frame"] = frnn_cuda.FrameInfo.from_workspace(ws[:4096].cpu().numpy())
+    out["stats"] = sws[:16 * D].cpu().numpy().view(np.float32).reshape(D, 4)
+    out["plan"], out["cells"] = plan, cells
+    return out
+
+
+def _near_pairs(X, radius, nq=400, seed=5):
+    """(q, p) pairs with exact fp32 distance < r2, for nq random queries."""
+    N = len(X)
+    rs = np.random.RandomState(seed)
+    r = float(np.float32(radius))
+    r2 = np.float32(np.float32(radius) ** 2)
+    X64 = X.astype(np.float64)
     n2 = np.sum(X64 ** 2, 1)
-    dmax = 0.0
-    for qb in np.array_split(rs.randint(0, N, 400), 8):
+    Q, P = [], []
+    for qb in np.array_split(rs.randint(0, N, nq), 8):
         near = (n2[None, :] + n2[qb, None] - 2 * X64[qb] @ X64.T) <= (1.01 * r) ** 2
         qq, pp = np.nonzero(near)
         qq = qb[qq]
-        inside = E.dist2(w.X[qq], w.X[pp], 0) < r2
-        qq, pp = qq[inside], pp[inside]
-        for s in (s0, s1):
-            dmax = max(dmax, float(np.max(np.abs(s[pp].astype(np.float64) - s[qq]))))
-    assert 0 < dmax <= r * (1 + 2.0 ** -15) + 2 * ri.margin
+        inside = E.dist2(X[qq], X[pp], 0) < r2
+        Q.append(qq[inside])
+        P.append(pp[inside])
+    return np.concatenate(Q), np.concatenate(P)
+
+
+@pytest.mark.parametrize("name,N", [("metric", 300_000), ("C3", 300_000)])
+def test_frame_grid_and_refinement(name, N):
+    """The grid frame of first-coordinate plans: descriptor (terms, directions,
+    margin, geometry), the binning recomputed in exact fp32, the guarantee that
+    pairs within the radius fall in neighbouring cells, the sub-bin order inside
+    big cells and the reorder invariants."""
+    w = W.config(name, N=N)
+    log(f"frame {name} N={N}")
+    out = _frame_build(w.X, w.K, w.radius)
+    fi, plan, cap = out["frame"], out["plan"], out["cells"]
+    g = plan.grid_dim
+    assert plan.path == 2 and g == 4 and fi.grid_dim == g and fi.projected == 1
+    st = out["stats"]
+    mean, var, lo, hi = (st[:, k] for k in range(4))
+    T = min(w.D, 32)
+    assert fi.terms == T and fi.axes == min(g + 2, T) - g
+    assert fi.bins0 * fi.bins1 == (1024 if fi.axes == 1 else 32 * 32)
+    # terms: the highest-variance coordinates, lower index on ties
+    coord = np.array(fi.coord[:T])
+    assert np.array_equal(coord, np.argsort(-var, kind="stable")[:T])
+    assert np.array_equal(np.array(fi.mean[:T], np.float32), mean[coord])
+    # directions: orthonormal up to the 1 - 2^-18 shrink; the grid block has
+    # spectral norm < 1, so projected gaps lower-bound distances
+    dirs = fi.directions()[:, :T].astype(np.float64)
+    slots = list(range(g)) + [4 + k for k in range(fi.axes)]
+    Wm = dirs[slots]
+    G = Wm @ Wm.T
+    assert np.all(np.abs(np.diag(G) - 1) < 1e-5) and np.all(np.diag(G) < 1)
+    assert np.max(np.abs(G - np.diag(np.diag(G)))) < 1e-5
+    assert np.linalg.norm(dirs[:g], 2) < 1
+    # the directions capture (nearly) the variance of the leading principal
+    # subspace (covariance from a sample of >= 128K points: 3% tolerance)
+    Y = (w.X[:, coord] - mean[coord]).astype(np.float64)
+    C = Y.T @ Y / N
+    ev = np.linalg.eigvalsh(C)[::-1]
+    captured = sum(wk @ C @ wk for wk in Wm)
+    assert captured >= 0.97 * ev[:len(slots)].sum(), (captured, ev[:len(slots) + 1])
+    for k in slots:
+        sg = np.sqrt(dirs[k] @ C @ dirs[k])
+        assert abs(fi.sigma[k] / sg - 1) <= 0.03
+    # margin >= (T + 2) u |x - mean| over the input
+    R = np.sqrt(np.sum(np.maximum(hi[coord].astype(np.float64) - mean[coord],
+                                  mean[coord] - lo[coord].astype(np.float64)) ** 2))
+    u = 2.0 ** -24
+    assert (T + 2) * u * R <= fi.margin <= 1.01 * (T + 2) * u * R
+    # geometry: cell edge >= r (1 + 2^-12) + 2 margin + 2 slack, binning
+    # reciprocal rounded down, origins at -4 sigma, grid within the capacity
+    r = float(np.float32(w.radius))
+    h0 = r * (1 + 2.0 ** -12) + 2 * fi.margin
+    smax = max(fi.sigma[k] for k in range(g))
+    assert fi.slack >= 2.0 ** -18 * (4 * smax + h0)
+    assert fi.h >= h0 + 2 * fi.slack and float(fi.inv_h) * float(fi.h) <= 1.0
+    res = np.array(fi.res[:g])
+    assert np.all(res >= 1) and fi.cells == np.prod(res) <= cap
+    assert list(fi.stride[:g]) == [int(np.prod(res[:d])) for d in range(g)]
+    for d in range(g):
+        assert fi.lo[d] == np.float32(-4.0 * np.float64(fi.sigma[d]))
+    # binning, recomputed in exact fp32
+    S = _project(w.X, fi, slots)
+    cc = np.stack([_sub_bins(S[d], fi.lo[d], fi.inv_h, fi.res[d]) for d in range(g)], 1)
+    cell_of = cc @ np.array(fi.stride[:g])
+    assert np.array_equal(out["cell_of"], cell_of)
+    cnt = np.bincount(cell_of, minlength=cap + 1)
+    assert np.array_equal(out["cnt"], cnt)
+    # the shell guarantee: pairs within the radius sit in neighbouring cells,
+    # and their projections differ by at most r (1 + 2^-15) + 2 margin
+    qq, pp = _near_pairs(w.X, w.radius)
+    assert len(qq) > 1000
+    assert np.max(np.abs(cc[qq] - cc[pp])) <= 1
+    for s in S:
+        assert np.max(np.abs(s[pp].astype(np.float64) - s[qq])) <= r * (1 + 2.0 ** -15) + 2 * fi.margin
     # reorder invariants
-    sidx, inv_p = sidx.cpu().numpy(), inv_p.cpu().numpy()
-    cnt = cnt.cpu().numpy()[:cells]
-    cells_of = O.bin_cells(w.X, g, res, np.float32(plan.inv_cell))
+    sidx, inv_p = out["sidx"], out["inv"]
     assert np.array_equal(np.sort(sidx), np.arange(N))
     assert np.array_equal(sidx[inv_p], np.arange(N))
-    cs = cells_of[sidx]
+    cs = cell_of[sidx]
     assert np.all(np.diff(cs) >= 0)
-    rows = aos.cpu().numpy().reshape(N, ds)
-    assert np.array_equal(rows[:, :w.D], w.X[sidx])
-    key = _sub_bins(s0[sidx], ri.lo0, ri.inv0, ri.bins0) * ri.bins1 + _sub_bins(s1[sidx], ri.lo1, ri.inv1, ri.bins1)
-    # filter rows: fl(x - mean) and their sequential-fma squared norms
-    fr = frows.cpu().numpy().reshape(N, ds)
+    ds = frnn_cuda.aos_stride(w.D)
+    assert np.array_equal(out["aos"].reshape(N, ds)[:, :w.D], w.X[sidx])
+    fr = out["frows"].reshape(N, ds)
     assert np.array_equal(fr[:, :w.D], (w.X[sidx] - mean[None, :]).astype(np.float32))
     assert np.all(fr[:, w.D:] == 0)
-    assert np.array_equal(fnorm.cpu().numpy(), E.dist2(fr, np.zeros_like(fr), 0))
+    assert np.array_equal(out["fnorm"], E.dist2(fr, np.zeros_like(fr), 0))
+    # sub-bin order inside cells holding >= 256 points
+    r0, r1 = S[g], S[g + 1] if fi.axes > 1 else np.zeros(N, np.float32)
+    key = _sub_bins(r0[sidx], fi.rlo0, fi.rinv0, fi.bins0) * fi.bins1
+    if fi.axes > 1:
+        key = key + _sub_bins(r1[sidx], fi.rlo1, fi.rinv1, fi.bins1)
     big = cnt[cs] >= 256
-    assert big.mean() > 0.5                      # most points live in refined cells here
     same_cell = np.concatenate([[False], cs[1:] == cs[:-1]])
     step = np.concatenate([[0], np.diff(key)])
     assert np.all(step[same_cell & big] >= 0)
-    # the keys are not all equal: the refinement splits the big cells
-    assert len(np.unique(key[big])) > 256
+    log(f"  res={list(res)} h/r={fi.h / r:.3f} cells={fi.cells} big-cell share={big.mean():.3f}")
+
+
+def test_frame_falls_back_to_raw_coordinates_on_infinite_input():
+    """An infinite coordinate makes the projection bound infinite: the frame
+    then bins the raw first g coordinates on the plan's own grid."""
+    rs = np.random.RandomState(12)
+    X = rs.rand(20000, 12).astype(np.float32)
+    X[17, 2] = np.inf
+    out = _frame_build(X, 16, 0.1)
+    fi, plan = out["frame"], out["plan"]
+    assert plan.path == 2 and fi.projected == 0 and fi.axes == 0
+    assert fi.cells == plan.cells and list(fi.res[:plan.grid_dim]) == [plan.res] * plan.grid_dim
+    want = O.bin_cells(X, plan.grid_dim, plan.res, np.float32(plan.inv_cell))
+    assert np.array_equal(out["cell_of"], want)
 
 
 def test_point_stats():

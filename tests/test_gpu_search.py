@@ -145,17 +145,48 @@ def test_engine_reuse_and_api():
 
 
 def test_profiling_counters_and_stage_times():
-    X = unit_cloud(20000, 16, 4, 2)
+    # raw grid: the shell counter equals the oracle's 3^D shell count
+    X = unit_cloud(20000, 3, 3, 2)
     eng = frnn_cuda.FRNNEngine(max_points=20000)
     eng.set_profiling(True)
     d = device_soa(X)
-    eng.search_gpu(d.data_ptr(), 20000, 16, 32, 0.15)
+    eng.search_gpu(d.data_ptr(), 20000, 3, 32, 0.05)
+    assert eng.last_plan()["path"] == "grid_full"
     st = eng.stage_times()
     c = eng.counters()
+    assert set(st) == set(frnn_cuda.STAGE_NAMES)
     assert st["search"] > 0 and all(v >= 0 for v in st.values())
-    assert c["shell_candidates"] == O.shell_candidates(X, 32, 0.15)
+    assert c["shell_candidates"] == O.shell_candidates(X, 32, 0.05)
     assert c["filter_hits"] >= c["accepted"] > 0
+    # framed first-coordinate grid: the frame stage runs; the shell is the
+    # frame's 3^g cells, and every accepted pair lies in it, was streamed and
+    # passed the filter
+    X = unit_cloud(20000, 16, 4, 2)
+    d = device_soa(X)
+    eng.search_gpu(d.data_ptr(), 20000, 16, 32, 0.15)
+    assert eng.last_plan()["path"] == "grid_first"
+    st = eng.stage_times()
+    c = eng.counters()
+    assert st["frame"] > 0 and st["refine"] > 0
+    assert c["shell_candidates"] >= c["accepted"]
+    assert c["streamed_pairs"] >= c["filter_hits"] >= c["accepted"] > 0
     eng.close()
+
+
+@pytest.mark.parametrize("bad", ["nan", "inf"])
+def test_nonfinite_points_on_a_framed_grid(bad):
+    # NaN: projections of such points are NaN (binned to cell 0, never within
+    # the radius); inf: the frame falls back to the raw first coordinates
+    X = unit_cloud(20000, 12, 3, 21)
+    X[5, 3] = np.nan if bad == "nan" else np.inf
+    X[9, :] = np.nan if bad == "nan" else -np.inf
+    X[11, 0] = np.nan if bad == "nan" else np.inf
+    log(f"non-finite {bad} on grid_first D=12")
+    gi, gd, plan = engine_search(X, 32, 0.1)
+    assert plan["path"] == "grid_first"
+    ri, rd = O.search(X, 32, 0.1)
+    assert_rows_equal(gi, gd, ri, rd, bad)
+    assert np.all(gi[9] == -1) and not np.any(gi == 9)
 
 
 def _golden_files():
