@@ -263,29 +263,40 @@ __global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restric
 // and |x - m|^2 <= sum_t max(hi_t - m_t, m_t - lo_t)^2 over the input.  A
 // non-finite bound (infinite input) is stored as +inf; frame_dirs_kernel then
 // falls back to the raw first coordinates.
-__global__ void frame_terms_kernel(const DimStat* __restrict__ st, int g, int D, Frame* __restrict__ f) {
-    if (threadIdx.x != 0) return;
+__global__ __launch_bounds__(128) void frame_terms_kernel(const DimStat* __restrict__ st, int g, int D,
+                                                          Frame* __restrict__ f) {
+    __shared__ float s_var[FRNN_MAX_DIM];
+    __shared__ int s_coord[kMaxTerms];
+    const int tid = threadIdx.x;
     const int T = D < kMaxTerms ? D : kMaxTerms;
-    unsigned long long taken0 = 0ull, taken1 = 0ull;
-    double R2 = 0.0;
-    for (int t = 0; t < kMaxTerms; ++t) {
-        f->coord[t] = 0;
-        f->mean[t] = 0.0f;
-        for (int k = 0; k < FRNN_FRAME_DIRS; ++k) f->dir[k][t] = 0.0f;
+    if (tid < D) s_var[tid] = st[tid].var;
+    for (int i = tid; i < kMaxTerms; i += blockDim.x) {
+        f->coord[i] = 0;
+        f->mean[i] = 0.0f;
     }
-    for (int t = 0; t < T; ++t) {
-        int best = -1;
-        for (int d = 0; d < D; ++d) {
-            const unsigned long long bit = 1ull << (d & 63);
-            if ((d < 64 ? taken0 : taken1) & bit) continue;
-            if (best < 0 || st[d].var > st[best].var) best = d;
+    for (int i = tid; i < FRNN_FRAME_DIRS * kMaxTerms; i += blockDim.x) (&f->dir[0][0])[i] = 0.0f;
+    __syncthreads();
+    // rank of coordinate tid in (variance descending, index ascending); the
+    // variances are never NaN (the statistics store -1 for NaN data)
+    if (tid < D) {
+        const float v = s_var[tid];
+        int rank = 0;
+        for (int e = 0; e < D; ++e) {
+            const float w = s_var[e];
+            rank += (w > v || (w == v && e < tid)) ? 1 : 0;
         }
-        if (best < 64) taken0 |= 1ull << best;
-        else taken1 |= 1ull << (best - 64);
-        const DimStat s = st[best];
-        f->coord[t] = best;
-        f->mean[t] = s.mean;
-        const double e = fmax((double)s.hi - (double)s.mean, (double)s.mean - (double)s.lo);
+        if (rank < T) s_coord[rank] = tid;
+    }
+    __syncthreads();
+    if (tid < T) {
+        f->coord[tid] = s_coord[tid];
+        f->mean[tid] = st[s_coord[tid]].mean;
+    }
+    if (tid != 0) return;
+    double R2 = 0.0;
+    for (int t = 0; t < T; ++t) {
+        const DimStat sd = st[s_coord[t]];
+        const double e = fmax((double)sd.hi - (double)sd.mean, (double)sd.mean - (double)sd.lo);
         R2 += e * e;
     }
     f->g = g;
@@ -372,6 +383,28 @@ __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts,
     }
 }
 
+// Sum of the covariance partials of pair blockIdx.x over the sampled tiles, in
+// a fixed order (strided per thread, then a tree), so the frame is
+// reproducible run to run.
+__global__ __launch_bounds__(256) void cov_reduce_kernel(const double* __restrict__ part, int nblk,
+                                                         const Frame* __restrict__ f,
+                                                         double* __restrict__ covsum) {
+    __shared__ double s_sum[256];
+    const int p = blockIdx.x;
+    const int T = f->terms;
+    if (p >= T * (T + 1) / 2) return;
+    const int tid = threadIdx.x;
+    double sum = 0.0;
+    for (int b = tid; b < nblk; b += 256) sum += part[(size_t)b * kMaxPairs + p];
+    s_sum[tid] = sum;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) s_sum[tid] += s_sum[tid + w];
+        __syncthreads();
+    }
+    if (tid == 0) covsum[p] = s_sum[0];
+}
+
 // Wave sum / max of a double through the lane exchanges (no LDS).
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -385,11 +418,10 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 
 // Principal directions and geometry of a frame (fp64, one wave; lane t holds
-// component t of every direction).  The covariance partials are reduced in a
-// fixed order; m = g + L leading eigenvectors come from subspace iteration
-// (modified Gram-Schmidt, iterates broadcast through LDS) and a final
-// Rayleigh-Ritz step (cyclic Jacobi on the m x m projected matrix, one
-// thread).  Directions 0..g-1 become the grid axes, the next L the refinement
+// component t of every direction).  The m = g + L leading eigenvectors of the
+// sampled covariance come from 16 steps of subspace iteration (modified
+// Gram-Schmidt, iterates broadcast through LDS) and a final Rayleigh-Ritz step
+// (cyclic Jacobi on the m x m projected matrix, in registers).  Directions 0..g-1 become the grid axes, the next L the refinement
 // directions (slots 4, 5); weights are scaled by 1 - 2^-18, so the fp32 grid
 // directions stay orthonormal up to a shrink (|U d| <= |d| for any d) and
 // every direction has norm < 1.
@@ -403,39 +435,30 @@ constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 // in the query's 3^g shell.  Refinement sub-bins span +-2.5 sigma.  An
 // infinite margin falls back to the raw first g coordinates with the plan's
 // cell size.
-__global__ __launch_bounds__(256) void frame_dirs_kernel(const double* __restrict__ part, int nblk,
-                                                         double nsamp, float radius, float cell_raw,
-                                                         float inv_cell_raw, int res_raw, int cells_cap,
-                                                         Frame* __restrict__ f) {
+__global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict__ covsum, double nsamp,
+                                                        float radius, float cell_raw, float inv_cell_raw,
+                                                        int res_raw, int cells_cap, Frame* __restrict__ f) {
     __shared__ double s_C[kMaxTerms][kMaxTerms + 1];
     __shared__ double s_v[kMaxDirs][kMaxTerms];
-    __shared__ double s_H[kMaxDirs][kMaxDirs];
-    __shared__ double s_R[kMaxDirs][kMaxDirs];
-    __shared__ int s_perm[kMaxDirs];
-    const int tid = threadIdx.x;
+    const int t = threadIdx.x;
     const int T = f->terms;
     const int g = f->g;
     const int m = g + f->L;
     const int P = T * (T + 1) / 2;
-    for (int p = tid; p < P; p += 256) {
-        double sum = 0.0;
-#pragma unroll 8
-        for (int b = 0; b < nblk; ++b) sum += part[(size_t)b * kMaxPairs + p];
+    for (int p = t; p < P; p += kWave) {
         int a, c;
         pair_of(p, T, a, c);
-        sum /= nsamp;
-        s_C[a][c] = sum;
-        s_C[c][a] = sum;
+        const double v = covsum[p] / nsamp;
+        s_C[a][c] = v;
+        s_C[c][a] = v;
     }
-    __syncthreads();
-    if (tid >= kWave) return;
-    const int t = tid;
     const bool on = t < T;
     auto lds_fence = [&]() {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
+    lds_fence();
     double v[kMaxDirs];
 #pragma unroll
     for (int j = 0; j < kMaxDirs; ++j)
@@ -488,14 +511,17 @@ __global__ __launch_bounds__(256) void frame_dirs_kernel(const double* __restric
             if (!on) w[j] = 0.0;
     };
     orthonormalise();
-    for (int it = 0; it < 24; ++it) {
+    for (int it = 0; it < 16; ++it) {
         double w[kMaxDirs];
         matvec(w);
 #pragma unroll
         for (int j = 0; j < kMaxDirs; ++j) v[j] = w[j];
         orthonormalise();
     }
-    // Rayleigh-Ritz: H = V^T C V, eigen-decomposed by cyclic Jacobi on lane 0
+    // Rayleigh-Ritz: H = V^T C V (wave sums, so every lane holds all of H),
+    // eigen-decomposed by cyclic Jacobi in registers, redundantly on every
+    // lane (identical operations, identical results)
+    double H[kMaxDirs][kMaxDirs], R[kMaxDirs][kMaxDirs];
     {
         double w[kMaxDirs];
         matvec(w);
@@ -503,76 +529,76 @@ __global__ __launch_bounds__(256) void frame_dirs_kernel(const double* __restric
         for (int j = 0; j < kMaxDirs; ++j)
 #pragma unroll
             for (int k = 0; k < kMaxDirs; ++k) {
-                if (j < m && k < m) {
-                    const double hjk = wave_sum_f64(v[j] * w[k]);
-                    if (t == 0) s_H[j][k] = hjk;
-                }
+                H[j][k] = (j < m && k < m) ? wave_sum_f64(v[j] * w[k]) : 0.0;
+                R[j][k] = (j == k) ? 1.0 : 0.0;
             }
     }
-    lds_fence();
-    if (t == 0) {
-        for (int j = 0; j < m; ++j)
-            for (int k = 0; k < m; ++k) s_R[j][k] = (j == k) ? 1.0 : 0.0;
-        for (int j = 0; j < m; ++j)
-            for (int k = j + 1; k < m; ++k) {
-                const double sym = 0.5 * (s_H[j][k] + s_H[k][j]);
-                s_H[j][k] = sym;
-                s_H[k][j] = sym;
-            }
-        for (int sweep = 0; sweep < 50; ++sweep) {
-            double off = 0.0, dia = 0.0;
-            for (int j = 0; j < m; ++j) {
-                dia += s_H[j][j] * s_H[j][j];
-                for (int k = j + 1; k < m; ++k) off += s_H[j][k] * s_H[j][k];
-            }
-            if (!(off > 1.0e-30 * dia) || !(off > 1.0e-300)) break;
-            for (int pp = 0; pp < m; ++pp)
-                for (int q = pp + 1; q < m; ++q) {
-                    const double apq = s_H[pp][q];
-                    if (!(fabs(apq) > 1.0e-300)) continue;
-                    const double th = (s_H[q][q] - s_H[pp][pp]) / (2.0 * apq);
+#pragma unroll
+    for (int j = 0; j < kMaxDirs; ++j)
+#pragma unroll
+        for (int k = j + 1; k < kMaxDirs; ++k) {
+            const double sym = 0.5 * (H[j][k] + H[k][j]);
+            H[j][k] = sym;
+            H[k][j] = sym;
+        }
+    for (int sweep = 0; sweep < 30; ++sweep) {
+        double off = 0.0, dia = 0.0;
+#pragma unroll
+        for (int j = 0; j < kMaxDirs; ++j) {
+            dia += H[j][j] * H[j][j];
+#pragma unroll
+            for (int k = j + 1; k < kMaxDirs; ++k) off += H[j][k] * H[j][k];
+        }
+        if (!(off > 1.0e-28 * dia) || !(off > 1.0e-300)) break;
+#pragma unroll
+        for (int pp = 0; pp < kMaxDirs; ++pp)
+#pragma unroll
+            for (int q = pp + 1; q < kMaxDirs; ++q) {
+                const double apq = H[pp][q];
+                if (q < m && fabs(apq) > 1.0e-300) {
+                    const double th = (H[q][q] - H[pp][pp]) / (2.0 * apq);
                     const double tt = (th >= 0.0 ? 1.0 : -1.0) / (fabs(th) + sqrt(th * th + 1.0));
                     const double cs = 1.0 / sqrt(tt * tt + 1.0), sn = tt * cs;
-                    for (int k = 0; k < m; ++k) {   // columns pp, q of H
-                        const double hkp = s_H[k][pp], hkq = s_H[k][q];
-                        s_H[k][pp] = cs * hkp - sn * hkq;
-                        s_H[k][q] = sn * hkp + cs * hkq;
+#pragma unroll
+                    for (int k = 0; k < kMaxDirs; ++k) {   // columns pp, q of H
+                        const double hkp = H[k][pp], hkq = H[k][q];
+                        H[k][pp] = cs * hkp - sn * hkq;
+                        H[k][q] = sn * hkp + cs * hkq;
                     }
-                    for (int k = 0; k < m; ++k) {   // rows pp, q of H
-                        const double hpk = s_H[pp][k], hqk = s_H[q][k];
-                        s_H[pp][k] = cs * hpk - sn * hqk;
-                        s_H[q][k] = sn * hpk + cs * hqk;
+#pragma unroll
+                    for (int k = 0; k < kMaxDirs; ++k) {   // rows pp, q of H
+                        const double hpk = H[pp][k], hqk = H[q][k];
+                        H[pp][k] = cs * hpk - sn * hqk;
+                        H[q][k] = sn * hpk + cs * hqk;
                     }
-                    for (int k = 0; k < m; ++k) {   // eigenvector columns
-                        const double rkp = s_R[k][pp], rkq = s_R[k][q];
-                        s_R[k][pp] = cs * rkp - sn * rkq;
-                        s_R[k][q] = sn * rkp + cs * rkq;
+#pragma unroll
+                    for (int k = 0; k < kMaxDirs; ++k) {   // eigenvector columns
+                        const double rkp = R[k][pp], rkq = R[k][q];
+                        R[k][pp] = cs * rkp - sn * rkq;
+                        R[k][q] = sn * rkp + cs * rkq;
                     }
                 }
-        }
-        // eigenvalues descending (ties: lower index first)
-        for (int j = 0; j < m; ++j) s_perm[j] = j;
-        for (int j = 0; j < m; ++j)
-            for (int k = j + 1; k < m; ++k)
-                if (s_H[s_perm[k]][s_perm[k]] > s_H[s_perm[j]][s_perm[j]]) {
-                    const int tmp = s_perm[j];
-                    s_perm[j] = s_perm[k];
-                    s_perm[k] = tmp;
-                }
+            }
     }
-    lds_fence();
+    // eigenvalues descending (ties: lower index first): selection by rank
+    double lam[kMaxDirs];
+#pragma unroll
+    for (int j = 0; j < kMaxDirs; ++j) lam[j] = H[j][j];
     constexpr double kShrink = 1.0 - 3.814697265625e-06;   // 1 - 2^-18
 #pragma unroll
-    for (int j = 0; j < kMaxDirs; ++j) {
-        if (j >= m) break;
-        const int col = s_perm[j];
+    for (int col = 0; col < kMaxDirs; ++col) {
+        if (col >= m) break;
+        int rank = 0;
+#pragma unroll
+        for (int k = 0; k < kMaxDirs; ++k)
+            if (k < m) rank += (lam[k] > lam[col] || (lam[k] == lam[col] && k < col)) ? 1 : 0;
         double u = 0.0;
 #pragma unroll
         for (int k = 0; k < kMaxDirs; ++k)
-            if (k < m) u = fma(s_R[k][col], v[k], u);
-        const int slot = j < g ? j : kRefDir0 + (j - g);
+            if (k < m) u = fma(R[k][col], v[k], u);
+        const int slot = rank < g ? rank : kRefDir0 + (rank - g);
         if (on) f->dir[slot][t] = (float)(u * kShrink);
-        if (t == 0) f->sigma[slot] = (float)sqrt(fmax(s_H[col][col], 0.0));
+        if (t == 0) f->sigma[slot] = (float)sqrt(fmax(lam[col], 0.0));
     }
     if (t != 0) return;
     // ---- geometry (one thread) ----
@@ -809,6 +835,7 @@ FrameLayout frame_layout(int N, int D, long long cells) {
     const int np = scan_partials_count(L.nsub > cells + 1 ? L.nsub : (int)(cells + 1));
     L.scanpart = off; off = align256(off + (size_t)np * sizeof(int));
     L.cov = off;      off = align256(off + (size_t)kCovBlocks * kMaxPairs * sizeof(double));
+    L.covsum = off;   off = align256(off + (size_t)kMaxPairs * sizeof(double));
     L.subkey = off;   off = align256(off + (size_t)N * sizeof(int));
     L.total = off;
     (void)D;
@@ -842,7 +869,7 @@ int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long l
     Frame* f = reinterpret_cast<Frame*>(base + L.frame);
     const DimStat* st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
     double* cov = reinterpret_cast<double*>(base + L.cov);
-    hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(64), 0, s, st, plan.grid_dim, D, f);
+    hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(128), 0, s, st, plan.grid_dim, D, f);
     // covariance sample: kCovBlocks tiles of 256 consecutive points, evenly spaced
     const long long tile_stride = N <= (long long)kCovBlocks * 256 ? 256 : (long long)N / kCovBlocks;
     long long nsamp = 0;
@@ -850,8 +877,10 @@ int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long l
         const long long i0 = (long long)b * tile_stride;
         nsamp += i0 < N ? (N - i0 < 256 ? N - i0 : 256) : 0;
     }
+    double* covsum = reinterpret_cast<double*>(base + L.covsum);
     hipLaunchKernelGGL(cov_kernel, dim3(kCovBlocks), dim3(256), 0, s, pts, N, tile_stride, f, cov);
-    hipLaunchKernelGGL(frame_dirs_kernel, dim3(1), dim3(256), 0, s, cov, kCovBlocks, (double)nsamp,
+    hipLaunchKernelGGL(cov_reduce_kernel, dim3(kMaxPairs), dim3(256), 0, s, cov, kCovBlocks, f, covsum);
+    hipLaunchKernelGGL(frame_dirs_kernel, dim3(1), dim3(kWave), 0, s, covsum, (double)nsamp,
                        plan.cell_size, plan.cell_size, plan.inv_cell, plan.res, (int)cells, f);
     return launch_result();
 }

@@ -54,7 +54,7 @@ struct Frame {
 static_assert(sizeof(Frame) == sizeof(frnn_frame_t), "Frame mirrors frnn_frame_t");
 
 struct FrameLayout {
-    size_t frame, bidx, subcnt, substart, scanpart, cov, subkey, total;   // byte offsets
+    size_t frame, bidx, subcnt, substart, scanpart, cov, covsum, subkey, total;   // byte offsets
     int max_big;        // upper bound on cells with >= kBigCell points
     int nsub;           // max_big * kSubBins + 1 scanned entries
 };

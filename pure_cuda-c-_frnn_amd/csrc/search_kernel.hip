@@ -595,12 +595,19 @@ void search_kernel(SearchArgs a) {
         };
 
         // One loop walks the segments (runs of queries sharing a row) and, per
-        // segment, batches of 64 traversal items; every iteration appends at
-        // most one run per lane and streams what is available, so the tile
-        // loop below is inlined once.
+        // segment, batches of 64 cells (one per lane); every iteration appends
+        // at most one run per lane and streams what is available, so the tile
+        // loop below is inlined once.  A refined cell whose window is narrower
+        // than the cell contributes one run per sub-bin row of the window, over
+        // successive iterations of the same batch.
         int seg = 0, seg_id = -1;
         int ib = 0, NI = 0;
+        int kk = 0, kmax = 0;               // sub-run index within the batch (wave-uniform)
         int xa = 0, nx = 1, nq1 = 1, qlo0 = 0, qlo1 = 0, qhi1 = 0, nb2 = 1;
+        bool windowed = false;              // the segment's window excludes some sub-bins
+        // this lane's cell of the current batch: sorted range, cell x, and the
+        // number of runs it contributes (0, 1, or nq1 for a windowed big cell)
+        int c_cell = 0, c_start = 0, c_end = 0, c_x = 0, c_runs = 0;
         float thr_seg = 0.0f;
         bool last = false;
         while (!last) {
@@ -672,59 +679,68 @@ void search_kernel(SearchArgs a) {
                 xa = max(xlo - 1, 0);
                 nx = min(xhi + 1, res0 - 1) - xa + 1;
                 nq1 = L > 0 ? max(qhi0 - qlo0 + 1, 0) : 1;
-                NI = nx * nrows * nq1;
+                windowed = L > 0 && (nq1 < fr->nb1 || qhi1 - qlo1 + 1 < nb2);
+                NI = nx * nrows;
                 ib = 0;
+                kk = 0;
             }
             if (ib < NI) {
-                const int item = ib + lane;
-                int rs = 0, rl = 0, rxv = 0;
-                if (item < NI) {
-                    const int q1i = item % nq1;
-                    const int rest = item / nq1;
-                    const int x = xa + rest % nx;
-                    int tt = rest / nx, Rb = 0;
-                    bool ok = true;
-                    // conservative AABB test of the whole cell against the
-                    // segment's queries
-                    float lb = 0.0f;
-                    {
-                        const float gp = axis_gap(0, x);
-                        lb = gp * gp;
-                    }
-                    for (int d = 1; d < G; ++d) {
-                        const int cc = s_rc[d] + (tt % 3) - 1;
-                        tt /= 3;
-                        const bool in = cc >= 0 && cc < s_res[d];
-                        ok = ok && in;
-                        Rb += cc * s_stride[d];
-                        if (in) {
-                            const float gp = axis_gap(d, cc);
-                            lb = fmaf(gp, gp, lb);
+                if (kk == 0) {
+                    // this lane's cell: AABB test against the segment's queries
+                    const int item = ib + lane;
+                    c_runs = 0;
+                    if (item < NI) {
+                        const int x = xa + item % nx;
+                        int tt = item / nx, Rb = 0;
+                        bool ok = true;
+                        float lb = 0.0f;
+                        {
+                            const float gp = axis_gap(0, x);
+                            lb = gp * gp;
                         }
-                    }
-                    rxv = x;
-                    if (ok) {
-                        const int c = x + Rb;
-                        const int cs = a.start[c];
-                        const int ce = a.start[c + 1];
-                        if (ce > cs && !(lb * keep > thr_seg)) {
-                            if (L > 0 && ce - cs >= kBigCell) {
-                                const int q1 = qlo0 + q1i;
-                                const size_t sb = (size_t)a.bidx[c] * kSubBins;
-                                const int s0 = a.substart[sb];
-                                const int sl = a.substart[sb + q1 * nb2 + qlo1];
-                                const int sh = a.substart[sb + q1 * nb2 + qhi1 + 1];
-                                rs = cs + (sl - s0);
-                                rl = sh - sl;
-                            } else if (q1i == 0) {
-                                rs = cs;
-                                rl = ce - cs;
+                        for (int d = 1; d < G; ++d) {
+                            const int cc = s_rc[d] + (tt % 3) - 1;
+                            tt /= 3;
+                            const bool in = cc >= 0 && cc < s_res[d];
+                            ok = ok && in;
+                            Rb += cc * s_stride[d];
+                            if (in) {
+                                const float gp = axis_gap(d, cc);
+                                lb = fmaf(gp, gp, lb);
                             }
                         }
+                        c_x = x;
+                        if (ok) {
+                            c_cell = x + Rb;
+                            c_start = a.start[c_cell];
+                            c_end = a.start[c_cell + 1];
+                            if (c_end > c_start && !(lb * keep > thr_seg))
+                                c_runs = (windowed && c_end - c_start >= kBigCell) ? nq1 : 1;
+                        }
+                    }
+                    kmax = wave_max_i32(c_runs);
+                }
+                int rs = 0, rl = 0;
+                if (kk < c_runs) {
+                    if (c_runs > 1 || (windowed && c_end - c_start >= kBigCell)) {
+                        // sub-bin row qlo0 + kk of the window, columns qlo1..qhi1
+                        const int q1 = qlo0 + kk;
+                        const size_t sb = (size_t)a.bidx[c_cell] * kSubBins;
+                        const int s0 = a.substart[sb];
+                        const int sl = a.substart[sb + q1 * nb2 + qlo1];
+                        const int sh = a.substart[sb + q1 * nb2 + qhi1 + 1];
+                        rs = c_start + (sl - s0);
+                        rl = sh - sl;
+                    } else {
+                        rs = c_start;
+                        rl = c_end - c_start;
                     }
                 }
-                append_runs(rs, rl, rxv, seg_id);
-                ib += kWave;
+                append_runs(rs, rl, c_x, seg_id);
+                if (++kk >= kmax) {
+                    kk = 0;
+                    ib += kWave;
+                }
             }
             last = ib >= NI && seg >= nq;
             consume(last);

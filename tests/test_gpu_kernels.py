@@ -15,7 +15,7 @@ import exact_fp32 as E
 import frnn_cuda
 import frnn_oracle as O
 import frnn_workloads as W
-from gpu_util import device_soa, log, torch, vp
+from gpu_util import assert_rows_equal, device_soa, log, torch, vp
 
 pytestmark = pytest.mark.gpu
 
@@ -318,3 +318,58 @@ def test_point_stats():
         assert abs(st[dd, 0] - X64[:, dd].mean()) <= 1e-6 * (1 + abs(X64[:, dd].mean()))
         assert abs(st[dd, 1] - X64[:, dd].var()) <= 1e-5 * X64[:, dd].var()
         assert st[dd, 2] == X[:, dd].min() and st[dd, 3] == X[:, dd].max()
+
+
+@pytest.mark.parametrize("framed", [True, False])
+def test_seam_search_first_coordinate_plan(framed):
+    """The whole search through the launch seam on a first-coordinate plan,
+    with the frame and without it (raw first coordinates, as the reference
+    bins them): both give the oracle's rows."""
+    t = torch()
+    rs = np.random.RandomState(31)
+    N, D, K, r = 30000, 12, 32, 0.1
+    X = rs.rand(N, D).astype(np.float32)
+    plan = frnn_cuda._plan_struct(N, D, K, r)
+    assert plan.path == 2
+    L = frnn_cuda._load()
+    ws_bytes = L.frnn_frame_workspace_bytes(N, D, ctypes.byref(plan))
+    assert ws_bytes > 0
+    d = device_soa(X)
+    cells = L.frnn_grid_cells(N, D, ctypes.byref(plan)) if framed else plan.cells
+    sws = t.zeros(L.frnn_stats_workspace_bytes(D), dtype=t.uint8, device="cuda:0")
+    assert L.frnn_launch_point_stats(vp(d), N, D, vp(sws), None) == 0
+    ws = None
+    if framed:
+        ws = t.zeros(ws_bytes, dtype=t.uint8, device="cuda:0")
+        assert L.frnn_launch_frame(vp(d), N, D, ctypes.byref(plan), vp(sws), vp(ws), None) == 0
+    cell_of = t.empty(N, dtype=t.int32, device="cuda:0")
+    rank = t.empty(N, dtype=t.int32, device="cuda:0")
+    cnt = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
+    assert L.frnn_launch_bin_count(vp(d), N, plan.grid_dim, plan.res, ctypes.c_float(plan.inv_cell), cells,
+                                   vp(ws), vp(cell_of), vp(rank), vp(cnt), None) == 0
+    start = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
+    part = t.empty(frnn_cuda.scan_partials_count(cells + 1), dtype=t.int32, device="cuda:0")
+    assert L.frnn_launch_exclusive_scan(vp(cnt), cells + 1, vp(start), vp(part), None) == 0
+    if framed:
+        assert L.frnn_launch_refine(vp(d), N, D, ctypes.byref(plan), vp(cell_of), vp(cnt), vp(rank), vp(ws),
+                                    None) == 0
+    ds = frnn_cuda.aos_stride(D)
+    sidx = t.empty(N, dtype=t.int32, device="cuda:0")
+    inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
+    aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
+    frows = t.empty(N * ds, dtype=t.float32, device="cuda:0")
+    fnorm = t.empty(N, dtype=t.float32, device="cuda:0")
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
+                                 vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), vp(fnorm), None) == 0
+    cap = frnn_cuda.list_capacity(K)
+    lists = t.empty(N * cap, dtype=t.int64, device="cuda:0")
+    assert L.frnn_launch_find_nbrs(vp(aos), vp(frows), vp(fnorm), vp(sidx), vp(cell_of), vp(start), vp(ws),
+                                   N, D, K, ctypes.byref(plan), vp(lists), cap, None, None) == 0
+    idx = t.empty(K * N, dtype=t.int32, device="cuda:0")
+    dist = t.empty(K * N, dtype=t.float32, device="cuda:0")
+    assert L.frnn_launch_unpermute(vp(lists), cap, vp(inv_p), N, K, vp(idx), vp(dist), None) == 0
+    t.cuda.synchronize()
+    gi = idx.cpu().numpy().reshape(K, N).T
+    gd = dist.cpu().numpy().reshape(K, N).T
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, f"seam framed={framed}")
