@@ -44,15 +44,15 @@ def eprint(*a):
 
 def build_bytes(N, D, ds, g, C, framed):
     """Algorithmic HBM bytes of each build kernel (4-byte ints and floats); ds is
-    the padded row length of the AoS and filter rows the reorder writes, C the
-    grid's cells (a frame's capacity for framed plans)."""
+    the padded row length of the AoS rows the reorder writes, C the grid's cells
+    (a frame's capacity for framed plans)."""
     T = min(D, 32)
     b = {
         "zero_fill": 4 * (C + 1),
         "stats": 4 * D * N,
         "bin_count": 4 * (T if framed else g) * N + 8 * N + 8 * (C + 1),
         "scan": 8 * (C + 1),
-        "reorder": 20 * N + 4 * D * N + 8 * ds * N + 4 * N,
+        "reorder": 20 * N + 4 * D * N + (8 if ds >= 64 else 4) * ds * N,
     }
     if framed:
         # frame: covariance sample over the T projection terms (512 tiles of 256
@@ -195,7 +195,8 @@ def main():
                          frnn_cuda.grid_cells(w.N, w.D, w.K, w.radius),
                          frnn_cuda.frame_workspace_bytes(w.N, w.D, w.K, w.radius) > 0)
     else:
-        bb = {"stats": 4 * w.D * w.N, "reorder": 4 * w.D * w.N + 8 * frnn_cuda.aos_stride(w.D) * w.N + 4 * w.N}
+        ds = frnn_cuda.aos_stride(w.D)
+        bb = {"stats": 4 * w.D * w.N, "reorder": 4 * w.D * w.N + (8 if ds >= 64 else 4) * ds * w.N}
     build = {}
     tot_b, tot_ms = 0, 0.0
     for k, b in bb.items():

@@ -61,8 +61,8 @@ typedef struct frnn_plan {
 typedef struct frnn_engine frnn_engine_t;
 
 /* Per-coordinate input statistics; a statistics workspace starts with
- * FRNN_MAX_DIM of them.  mean is the centre of the MFMA filter rows (0 if not
- * finite), var/lo/hi choose and scale the refinement axes. */
+ * FRNN_MAX_DIM of them.  mean is the centre of the MFMA filter operands (0 if
+ * not finite), var/lo/hi choose the frame's terms and bound its projections. */
 typedef struct frnn_dim_stat {
     float mean, var, lo, hi;
 } frnn_dim_stat_t;
@@ -224,36 +224,41 @@ int frnn_launch_refine(const float* d_points_soa, int N, int dim, const frnn_pla
 /* run_counting_sort / run_counting_sort_aos3 (insert_points.cu:142-164,205-226):
  * pos = d_start[cell] + rank (+ the sub-bin offset inside refined cells);
  * d_sorted_idx[pos] = i; d_inv[i] = pos; AoS row pos of d_sorted_aos (stride
- * frnn_aos_stride(dim), zero padded) = point i.  With d_stats_ws, row pos of
- * d_frows gets fl(x - mean) and d_fnorm[pos] its squared norm (the MFMA filter
- * operands).  d_frame_ws and d_stats_ws may be NULL; cells as frnn_grid_cells. */
+ * frnn_aos_stride(dim), zero padded) = point i.  With d_frows (needs
+ * d_stats_ws), row pos of d_frows also gets the centred row fl(x - mean), which
+ * the search streams when frnn_uses_filter_rows(dim).  d_frame_ws, d_stats_ws
+ * and d_frows may be NULL; cells as frnn_grid_cells. */
 int frnn_launch_reorder(const float* d_points_soa, int N, int dim, const int* d_cell_of,
                         const int* d_rank, const int* d_start, const int* d_cnt,
                         const void* d_frame_ws, long long cells, int* d_sorted_idx, int* d_inv,
-                        float* d_sorted_aos, const void* d_stats_ws, float* d_frows, float* d_fnorm,
-                        void* stream);
+                        float* d_sorted_aos, const void* d_stats_ws, float* d_frows, void* stream);
 
 /* Brute-force input staging: AoS copy of the SoA points in original order,
- * plus the filter rows and norms as frnn_launch_reorder when d_stats_ws is given. */
+ * plus the centred rows as frnn_launch_reorder when d_frows is given. */
 int frnn_launch_transpose(const float* d_points_soa, int N, int dim, float* d_aos,
-                          const void* d_stats_ws, float* d_frows, float* d_fnorm, void* stream);
+                          const void* d_stats_ws, float* d_frows, void* stream);
+
+/* 1 when the search streams precomputed centred filter rows for this dim
+ * (padded rows of 64 floats or more), 0 when it centres rows in registers. */
+int frnn_uses_filter_rows(int dim);
 
 /* run_find_nbrs / run_find_nbrs_griddim / run_find_nbrs_aos3 / run_bruteforce
  * (find_nbrs.cu:525-633, no_grid_frnn.cu:273-326): neighbour search over the
- * plan's path.  The MFMA filter streams d_frows/d_fnorm (written by the reorder
- * or transpose with statistics); exact distances use d_aos.  Grid paths read
- * the cell-sorted AoS points, d_sorted_idx, d_cell_of (cell id per original
+ * plan's path.  The MFMA filter works on rows centred on the means of
+ * d_stats_ws (frnn_launch_point_stats): d_frows (required when
+ * frnn_uses_filter_rows(dim), ignored otherwise) or the AoS rows centred as
+ * they are loaded; exact distances use the raw AoS rows.  Grid paths read the
+ * cell-sorted AoS points, d_sorted_idx, d_cell_of (cell id per original
  * point), d_start (frnn_grid_cells + 1 exclusive offsets) and, for
  * first-coordinate plans, the frame workspace; brute force reads the
- * transposed AoS points and ignores them.  Results: for sorted position s, entries
- * d_lists[s*list_cap + k], k < K, hold ascending keys (bits(d2) << 32 | idx)
- * with padding (bits(r2) << 32 | 0xffffffff).  d_counters (5 u64: the
- * FRNN_NUM_COUNTERS work counters and a capacity-guard counter; may be NULL)
- * accumulates the counters. */
-int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float* d_fnorm,
+ * transposed AoS points and ignores them.  Results: for sorted position s,
+ * entries d_lists[s*list_cap + k], k < K, hold ascending keys
+ * (bits(d2) << 32 | idx) with padding (bits(r2) << 32 | 0xffffffff).
+ * d_counters (5 u64: the FRNN_NUM_COUNTERS work counters and a capacity-guard
+ * counter; may be NULL) accumulates the counters. */
+int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const void* d_stats_ws,
                           const int* d_sorted_idx, const int* d_cell_of, const int* d_start,
-                          const void* d_frame_ws,
-                          int N, int dim, int K, const frnn_plan_t* plan,
+                          const void* d_frame_ws, int N, int dim, int K, const frnn_plan_t* plan,
                           unsigned long long* d_lists, int list_cap,
                           unsigned long long* d_counters, void* stream);
 

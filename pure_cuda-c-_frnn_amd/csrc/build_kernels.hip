@@ -124,15 +124,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_final_kernel(const int* __r
     }
 }
 
-// Row `pos` of the AoS array gets point i (zero padded to ds); when filter
-// rows are requested, row `pos` of frows gets fl(x - mean) and fnorm[pos] its
-// squared norm (sequential fma).
-__device__ __forceinline__ void write_rows(const float* __restrict__ pts, int N, int D, int ds, int i, int pos,
-                                           float* __restrict__ aos, const DimStat* __restrict__ st,
-                                           float* __restrict__ frows, float* __restrict__ fnorm) {
+// Row `pos` of the AoS array gets point i (zero padded to ds); with frows,
+// row `pos` of frows also gets the centred row fl(x - mean) (zero padded).
+__device__ __forceinline__ void write_row(const float* __restrict__ pts, int N, int D, int ds, int i, int pos,
+                                          float* __restrict__ aos, const DimStat* __restrict__ st,
+                                          float* __restrict__ frows) {
     float4* row = reinterpret_cast<float4*>(aos + (size_t)pos * ds);
     float4* frow = frows ? reinterpret_cast<float4*>(frows + (size_t)pos * ds) : nullptr;
-    float nrm = 0.0f;
     for (int d = 0; d < ds; d += 4) {
         float4 v;
         v.x = (d + 0 < D) ? pts[(size_t)(d + 0) * N + i] : 0.0f;
@@ -147,13 +145,8 @@ __device__ __forceinline__ void write_rows(const float* __restrict__ pts, int N,
             f.z = (d + 2 < D) ? v.z - st[d + 2].mean : 0.0f;
             f.w = (d + 3 < D) ? v.w - st[d + 3].mean : 0.0f;
             frow[d >> 2] = f;
-            nrm = fmaf(f.x, f.x, nrm);
-            nrm = fmaf(f.y, f.y, nrm);
-            nrm = fmaf(f.z, f.z, nrm);
-            nrm = fmaf(f.w, f.w, nrm);
         }
     }
-    if (frow) fnorm[pos] = nrm;
 }
 
 // One thread per point: SoA reads are coalesced per axis; the AoS row store
@@ -172,8 +165,7 @@ __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ 
                                                       int* __restrict__ inv,
                                                       float* __restrict__ aos,
                                                       const DimStat* __restrict__ st,
-                                                      float* __restrict__ frows,
-                                                      float* __restrict__ fnorm) {
+                                                      float* __restrict__ frows) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
     const int c = cell_of[i];
@@ -184,7 +176,7 @@ __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ 
     }
     sorted_idx[pos] = i;
     inv[i] = pos;
-    write_rows(pts, N, D, ds, i, pos, aos, st, frows, fnorm);
+    write_row(pts, N, D, ds, i, pos, aos, st, frows);
 }
 
 // Per-coordinate statistics.  Block (b, d) reduces coordinate d over its
@@ -735,11 +727,10 @@ __global__ __launch_bounds__(256) void sub_count_kernel(const float* __restrict_
 __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ pts, int N, int D, int ds,
                                                         float* __restrict__ aos,
                                                         const DimStat* __restrict__ st,
-                                                        float* __restrict__ frows,
-                                                        float* __restrict__ fnorm) {
+                                                        float* __restrict__ frows) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
-    write_rows(pts, N, D, ds, i, i, aos, st, frows, fnorm);
+    write_row(pts, N, D, ds, i, i, aos, st, frows);
 }
 
 // Output transpose through LDS, 32 original queries per workgroup: the K keys
@@ -907,10 +898,16 @@ int launch_refine(const float* pts, int N, int D, long long cells, const int* ce
     return launch_result();
 }
 
+static const DimStat* stats_of(const void* stats_ws, int D) {
+    return stats_ws ? reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims)
+                    : nullptr;
+}
+
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,
                    const int* cnt, const void* frame_ws, long long cells, int* sorted_idx, int* inv,
-                   float* aos, const void* stats_ws, float* frows, float* fnorm, hipStream_t s) {
+                   float* aos, const void* stats_ws, float* frows, hipStream_t s) {
     if (N <= 0) return 0;
+    if (frows && !stats_ws) return 1;
     const int* subkey = nullptr;
     const int* bidx = nullptr;
     const int* substart = nullptr;
@@ -921,25 +918,18 @@ int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int
         bidx = reinterpret_cast<const int*>(base + L.bidx);
         substart = reinterpret_cast<const int*>(base + L.substart);
     }
-    const DimStat* st = stats_ws ? reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) +
-                                                                    stats_layout(D).dims)
-                                 : nullptr;
-    if (!st) frows = nullptr;
     hipLaunchKernelGGL(reorder_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, D,
                        aos_stride(D), cell_of, rank, start, cnt, subkey, bidx, substart, sorted_idx, inv, aos,
-                       st, frows, fnorm);
+                       stats_of(stats_ws, D), frows);
     return launch_result();
 }
 
 int launch_transpose(const float* pts, int N, int D, float* aos, const void* stats_ws, float* frows,
-                     float* fnorm, hipStream_t s) {
+                     hipStream_t s) {
     if (N <= 0) return 0;
-    const DimStat* st = stats_ws ? reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) +
-                                                                    stats_layout(D).dims)
-                                 : nullptr;
-    if (!st) frows = nullptr;
+    if (frows && !stats_ws) return 1;
     hipLaunchKernelGGL(transpose_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, D,
-                       aos_stride(D), aos, st, frows, fnorm);
+                       aos_stride(D), aos, stats_of(stats_ws, D), frows);
     return launch_result();
 }
 

@@ -102,11 +102,9 @@ struct frnn_engine {
     void* frame_ws = nullptr;     // grid frame and within-cell refinement tables
     size_t frame_bytes = 0;
     void* stats_ws = nullptr;     // per-coordinate statistics (filter centre, frame terms)
-    size_t stats_bytes = 0;
-    float* frows = nullptr;       // centred filter rows, stride aos_stride(dim)
+    float* frows = nullptr;       // centred filter rows (wide rows only), stride aos_stride(dim)
     size_t frows_bytes = 0;
-    float* fnorm = nullptr;       // their squared norms
-    size_t fnorm_bytes = 0;
+    size_t stats_bytes = 0;
     unsigned long long* lists = nullptr;
     size_t lists_bytes = 0;
     float* h2d_points = nullptr;  // search() staging (frnn_engine.cu:27 d_points)
@@ -125,7 +123,7 @@ namespace {
 void release(frnn_engine* e) {
     void* bufs[] = {e->cell_of, e->rank, e->sorted_idx, e->inv, e->cnt, e->start, e->partials,
                     e->counters, e->out_idx, e->out_dist, e->aos, e->lists, e->h2d_points,
-                    e->frame_ws, e->stats_ws, e->frows, e->fnorm};
+                    e->frame_ws, e->stats_ws, e->frows};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (auto& ev : e->ev)
@@ -147,10 +145,13 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     const int ds = frnn::aos_stride(dim);
     const int cap = frnn::list_capacity(K);
     ST_TRY(grow(&e->aos, &e->aos_bytes, (size_t)N * ds, "allocating AoS point rows"));
-    ST_TRY(grow(&e->frows, &e->frows_bytes, (size_t)N * ds, "allocating filter rows"));
-    ST_TRY(grow(&e->fnorm, &e->fnorm_bytes, (size_t)N, "allocating filter norms"));
     ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)N * cap, "allocating candidate lists"));
     ST_TRY(grow((char**)&e->stats_ws, &e->stats_bytes, frnn::stats_layout(dim).total, "allocating statistics"));
+    float* frows = nullptr;
+    if (frnn::uses_filter_rows(dim)) {
+        ST_TRY(grow(&e->frows, &e->frows_bytes, (size_t)N * ds, "allocating filter rows"));
+        frows = e->frows;
+    }
 
     hipStream_t s = e->stream;
     const bool grid = plan.path != FRNN_PATH_BRUTEFORCE;
@@ -200,18 +201,18 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
                              "refinement launch"));
     ST_TRY(mark(6));
     // stage 6: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
-    // brute force, the AoS copy; both also write the filter rows
+    // brute force, the AoS copy
     if (grid)
         ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start, e->cnt,
-                                                  frame, cells, e->sorted_idx, e->inv, e->aos,
-                                                  e->stats_ws, e->frows, e->fnorm, s),
+                                                  frame, cells, e->sorted_idx, e->inv, e->aos, e->stats_ws,
+                                                  frows, s),
                              "reorder launch"));
     else
-        ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, e->stats_ws, e->frows, e->fnorm, s),
+        ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, e->stats_ws, frows, s),
                              "transpose launch"));
     ST_TRY(mark(7));
     // stage 7: neighbour search
-    ST_TRY(launch_status(frnn::launch_search(e->aos, e->frows, e->fnorm, grid ? e->sorted_idx : nullptr,
+    ST_TRY(launch_status(frnn::launch_search(e->aos, frows, e->stats_ws, grid ? e->sorted_idx : nullptr,
                                              grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
                                              N, dim, K, plan, e->lists, cap,
                                              e->profiling ? e->counters : nullptr, s),
@@ -547,33 +548,37 @@ int frnn_launch_refine(const float* d_pts, int N, int dim, const frnn_plan_t* pl
                          "refinement launch");
 }
 
+int frnn_uses_filter_rows(int dim) {
+    if (dim < 1 || dim > FRNN_MAX_DIM) return -1;
+    return frnn::uses_filter_rows(dim) ? 1 : 0;
+}
+
 int frnn_launch_reorder(const float* d_pts, int N, int dim, const int* d_cell_of, const int* d_rank,
                         const int* d_start, const int* d_cnt, const void* d_frame_ws, long long cells,
                         int* d_sorted_idx, int* d_inv, float* d_sorted_aos, const void* d_stats_ws,
-                        float* d_frows, float* d_fnorm, void* stream) {
+                        float* d_frows, void* stream) {
     if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
     if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_start || !d_sorted_idx || !d_inv || !d_sorted_aos))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
     if (d_frame_ws && (!d_cnt || cells < 1 || cells > FRNN_MAX_CELLS))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame needs the counts and the cell count");
-    if (d_stats_ws && (!d_frows || !d_fnorm)) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need both outputs");
+    if (d_frows && !d_stats_ws) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need the statistics");
     return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_cnt, d_frame_ws,
                                               cells, d_sorted_idx, d_inv, d_sorted_aos, d_stats_ws, d_frows,
-                                              d_fnorm, (hipStream_t)stream),
+                                              (hipStream_t)stream),
                          "reorder launch");
 }
 
 int frnn_launch_transpose(const float* d_pts, int N, int dim, float* d_aos, const void* d_stats_ws,
-                          float* d_frows, float* d_fnorm, void* stream) {
+                          float* d_frows, void* stream) {
     if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
     if (N > 0 && (!d_pts || !d_aos)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    if (d_stats_ws && (!d_frows || !d_fnorm)) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need both outputs");
-    return launch_status(frnn::launch_transpose(d_pts, N, dim, d_aos, d_stats_ws, d_frows, d_fnorm,
-                                                (hipStream_t)stream),
+    if (d_frows && !d_stats_ws) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need the statistics");
+    return launch_status(frnn::launch_transpose(d_pts, N, dim, d_aos, d_stats_ws, d_frows, (hipStream_t)stream),
                          "transpose launch");
 }
 
-int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float* d_fnorm,
+int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const void* d_stats_ws,
                           const int* d_sorted_idx, const int* d_cell_of, const int* d_start,
                           const void* d_frame_ws, int N, int dim, int K, const frnn_plan_t* plan,
                           unsigned long long* d_lists, int list_cap, unsigned long long* d_counters,
@@ -583,8 +588,10 @@ int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float*
     if (plan->path == FRNN_PATH_EMPTY || N == 0) return FRNN_OK;
     if (list_cap < frnn::list_capacity(K)) return fail(FRNN_ERR_INVALID_ARGUMENT, "list_cap too small");
     const bool grid = plan->path != FRNN_PATH_BRUTEFORCE;
-    if (!d_aos || !d_frows || !d_fnorm || !d_lists || (grid && (!d_sorted_idx || !d_cell_of || !d_start)))
+    if (!d_aos || !d_stats_ws || !d_lists || (grid && (!d_sorted_idx || !d_cell_of || !d_start)))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (frnn::uses_filter_rows(dim) && !d_frows)
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "this dimension needs the centred filter rows");
     if (grid && (plan->grid_dim < 1 || plan->grid_dim > 9 || plan->grid_dim > dim || plan->res < 1 ||
                  ipow_sat(plan->res, plan->grid_dim, (long long)4e18) != plan->cells ||
                  plan->cells > FRNN_MAX_CELLS))
@@ -592,7 +599,7 @@ int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const float*
     if (plan->rev_order && (!grid || dim != 3)) return fail(FRNN_ERR_INVALID_ARGUMENT, "reversed order is D=3 grid only");
     if (d_frame_ws && !frnn::has_frame(*plan, dim))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame given for a plan without one");
-    return launch_status(frnn::launch_search(d_aos, d_frows, d_fnorm, d_sorted_idx, d_cell_of, d_start,
+    return launch_status(frnn::launch_search(d_aos, d_frows, d_stats_ws, d_sorted_idx, d_cell_of, d_start,
                                              d_frame_ws, N, dim, K, *plan, d_lists, list_cap, d_counters,
                                              (hipStream_t)stream),
                          "search launch");

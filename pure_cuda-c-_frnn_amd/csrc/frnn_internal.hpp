@@ -100,19 +100,24 @@ int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, co
                      int cells, int* cell_of, int* rank, int* cnt, hipStream_t s);
 // flag_min > 0 scans (in[i] >= flag_min) instead of in[i]
 int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s, int flag_min = 0);
-// frame_ws: the frame workspace (refined big cells), or nullptr.
-// stats_ws/frows/fnorm: when given, also write the centred filter rows
-// fl(x - mean) (stride aos_stride(D)) and their squared norms.
+// frame_ws: the frame workspace (refined big cells), or nullptr.  With
+// frows (which needs stats_ws) the centred filter rows fl(x - mean) are
+// written too.
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,
                    const int* cnt, const void* frame_ws, long long cells, int* sorted_idx, int* inv,
-                   float* aos, const void* stats_ws, float* frows, float* fnorm, hipStream_t s);
+                   float* aos, const void* stats_ws, float* frows, hipStream_t s);
 int launch_transpose(const float* pts, int N, int D, float* aos, const void* stats_ws, float* frows,
-                     float* fnorm, hipStream_t s);
+                     hipStream_t s);
+// Wide rows (padded length >= 64) stream precomputed centred filter rows;
+// narrower rows are centred in registers as they are loaded.
+inline bool uses_filter_rows(int D) { return aos_stride(D) >= 64; }
 int launch_unpermute(const unsigned long long* lists, int cap, const int* inv, int N, int K, int* idxs,
                      float* dists, hipStream_t s);
-int launch_search(const float* aos, const float* frows, const float* fnorm, const int* sorted_idx,
-                  const int* cell_of, const int* start, const void* frame_ws, int N, int D, int K,
-                  const frnn_plan_t& plan, unsigned long long* lists, int cap, unsigned long long* counters,
-                  hipStream_t s);
+// stats_ws: the point statistics (the per-coordinate means centre the MFMA
+// filter operands).
+int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
+                  const int* cell_of,
+                  const int* start, const void* frame_ws, int N, int D, int K, const frnn_plan_t& plan,
+                  unsigned long long* lists, int cap, unsigned long long* counters, hipStream_t s);
 
 }  // namespace frnn

@@ -17,12 +17,13 @@
 //   * candidates stream through in tiles of 32.  The distance tile
 //     32 candidates x 32 queries is one chain of v_mfma_f32_32x32x2f32 on the
 //     augmented vectors  a = [p', |p'|^2, 1],  b = [-2q', 1-c, (1-c)|q'|^2]
-//     (p', q' the rows centred on the input mean, precomputed with their norms
-//     by the reorder), so the accumulator is a filter value F <= the exact
-//     distance plus a proven rounding bound;
+//     (p', q' the rows centred on the input mean as they are loaded, with
+//     their squared norms), so the accumulator is a filter value F <= the
+//     exact distance plus a proven rounding bound;
 //   * pairs with F below the query's threshold (plus a relative margin) are
 //     queued in LDS and re-evaluated 64 at a time with the reference's exact fp32
-//     distance order; accepted (d2, idx) keys go to a per-query candidate list;
+//     distance order on the raw rows (the lines the filter just gathered);
+//     accepted (d2, idx) keys go to a per-query candidate list;
 //   * when a list nears capacity the wave sorts it cooperatively (bitonic in
 //     registers, up to 4 keys per lane), keeps the K smallest and tightens the
 //     query's threshold to the K-th key; at the end every list is sorted and its
@@ -61,8 +62,8 @@ constexpr int kMaxG = 9;
 
 struct SearchArgs {
     const float* pts;            // AoS rows, stride DS (sorted order for grids)
-    const float* frows;          // the same rows centred on the input mean: fl(x - mean)
-    const float* fnorm;          // squared norms of the centred rows
+    const float* frows;          // the same rows centred, fl(x - mean) (wide rows only)
+    const DimStat* st;           // per-coordinate statistics: the filter centre is the mean
     const int* sorted_idx;       // sorted position -> original index (grid paths)
     const int* cell_of;          // original index -> cell id (grid paths)
     const int* start;            // cells+1 exclusive cell offsets (grid paths)
@@ -71,7 +72,7 @@ struct SearchArgs {
     const int* substart;         // sub-bin offsets of big cells
     unsigned long long* lists;   // [N][cap] candidate keys
     unsigned long long* counters;
-    int N, K, cap, G, res;       // res: raw-grid cells per axis
+    int N, D, K, cap, G, res;    // res: raw-grid cells per axis
     int gstride[kMaxG];          // raw-grid cell-id stride per axis
     int room;                    // usable list entries: min(cap, largest register sort)
     float r2, cell, radius;      // cell: raw-grid cell edge
@@ -133,19 +134,32 @@ void search_kernel(SearchArgs a) {
     constexpr bool PREFETCH = DS <= 32;
     // The chunk's query rows: staged in LDS for DS <= 32; wider rows are read
     // from the AoS array (the same 32 rows, cache resident), which keeps LDS
-    // small enough for two workgroups per SIMD.
+    // small enough for two workgroups per SIMD.  LDS rows are RS floats apart:
+    // DS padded by 4 when DS is a multiple of 8, so the 16-byte reads of
+    // different rows spread over all eight 4-bank groups.
     constexpr bool kQueryLds = DS <= 32;
-    __shared__ __align__(16) float s_q[kQueryLds ? kQB * DS : 4];
+    constexpr int RS = (DS % 8 == 0) ? DS + 4 : DS;
+    __shared__ __align__(16) float s_q[kQueryLds ? kQB * RS : 4];
     __shared__ int s_cnt[kQB];
     __shared__ int s_srt[kQB];       // sorted prefix length of each list
     __shared__ unsigned long long s_thr[kQB];
-    __shared__ unsigned char s_qn[kQueueCap];
-    __shared__ int s_qpos[kQueueCap];
+    // Rows of up to 32 floats re-evaluate a tile's hits right after its MFMA
+    // chain, from the tile's raw rows staged in LDS; wider rows queue hits as
+    // (query, sorted position) and re-evaluate them 64 at a time from memory.
+    constexpr bool kTileExact = DS <= 32;
+    __shared__ unsigned char s_qn[kTileExact ? 1 : kQueueCap];
+    __shared__ int s_qpos[kTileExact ? 1 : kQueueCap];
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points,
     // virtual stream positions [vbeg, vend), cell x and row-segment id
     __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing], r_x[kRing], r_seg[kRing];
-    // current tile: candidate row -> sorted position, cell x, segment id
-    __shared__ int t_pos[32], t_x[32], t_seg[32];
+    // current tile, per candidate row: the packed (segment, cell x) shell key
+    // and the original index (tile-exact path) or sorted position (queue
+    // path); tile-exact path: the raw rows (stride RS, as s_q) and the hit
+    // entries (row << 5 | query)
+    __shared__ int t_idx[32], t_sx[32];
+    __shared__ int t_pos[kTileExact ? 1 : 32];
+    __shared__ __align__(16) float t_rows[kTileExact ? 32 * RS : 4];
+    __shared__ unsigned short s_hit[kTileExact ? 32 * 32 : 2];
     // grid geometry per axis (cells, cell-id stride, origin), the segment's
     // bounding box and row coordinates, and each query's grid coordinates
     __shared__ int s_res[kMaxG], s_stride[kMaxG];
@@ -170,7 +184,7 @@ void search_kernel(SearchArgs a) {
 
     if constexpr (kQueryLds) {
         const float* src = a.pts + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
-        float* dst = s_q + n * DS + h * HD;
+        float* dst = s_q + n * RS + h * HD;
 #pragma unroll
         for (int j = 0; j < HD; j += 2) {
             float2 v = *reinterpret_cast<const float2*>(src + j);
@@ -179,30 +193,51 @@ void search_kernel(SearchArgs a) {
             dst[j + 1] = v.y;
         }
     }
-    // row of query qn (a valid query of the chunk)
-    auto query_row = [&](int qn) -> const float* {
-        if constexpr (kQueryLds) return s_q + qn * DS;
-        else return a.pts + (size_t)(q0 + qn) * DS;
-    };
+    // row of query qn (a valid query of the chunk; queue path, wide rows)
+    auto query_row = [&](int qn) -> const float* { return a.pts + (size_t)(q0 + qn) * DS; };
     if (lane < kQB) {
         s_cnt[lane] = 0;
         s_srt[lane] = 0;
         s_thr[lane] = make_key(a.r2, 0);
     }
     lds_sync();
+    // Filter operands are the rows centred on the input mean, fl(x - mean).
+    // Rows of up to 32 floats are centred in registers as they are loaded
+    // (this lane's half of the means stays in registers); wider rows stream
+    // the centred copy the reorder wrote, which keeps their loads ahead of the
+    // MFMA chain.
+    constexpr bool kCentredRows = DS >= 64;
+    float mh[kCentredRows ? 1 : HD];
+    if constexpr (!kCentredRows) {
+#pragma unroll
+        for (int j = 0; j < HD; ++j) {
+            const int d = h * HD + j;
+            mh[j] = d < a.D ? a.st[d].mean : 0.0f;
+        }
+    }
+    const float* const op_rows = kCentredRows ? a.frows : a.pts;
+    auto centre = [&](float x, int j) __attribute__((always_inline)) -> float {
+        if constexpr (kCentredRows) return x;
+        else return x - mh[j];
+    };
     // B operand: this lane's half of query n's centred row, scaled by -2, plus
-    // the norm column.  Rows of a chunk are the sorted points q0..q0+31.
+    // the norm column (the squared norm of the centred row, summed from both
+    // halves).  Rows of a chunk are the sorted points q0..q0+31.
     float bop[HD + 1];
     float qn2 = 0.0f;
     {
-        const float* fr = a.frows + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
+        const float* qr = op_rows + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
+        float pn = 0.0f;
 #pragma unroll
         for (int j = 0; j < HD; j += 2) {
-            const float2 v = *reinterpret_cast<const float2*>(fr + j);
-            bop[j] = -2.0f * v.x;
-            bop[j + 1] = -2.0f * v.y;
+            const float2 v = *reinterpret_cast<const float2*>(qr + j);
+            const float c0 = centre(v.x, j), c1 = centre(v.y, j + 1);
+            bop[j] = -2.0f * c0;
+            bop[j + 1] = -2.0f * c1;
+            pn = fmaf(c0, c0, pn);
+            pn = fmaf(c1, c1, pn);
         }
-        qn2 = a.fnorm[q0 + (qvalid ? n : 0)];
+        qn2 = pn + __shfl_xor(pn, 32);
         bop[HD] = (h == 0) ? a.norm_scale : qn2 * a.norm_scale;
     }
     if (!qvalid) {
@@ -302,9 +337,9 @@ void search_kernel(SearchArgs a) {
         }
     };
 
-    // Exact re-evaluation of queue entries [base, base + count).  First every
-    // list that could overflow during the batch is compacted; with final_pass
-    // every list of the chunk gets its final selection instead.
+    // Exact re-evaluation of queue entries [base, base + count) (queue path).
+    // First every list that could overflow during the batch is compacted; with
+    // final_pass every list of the chunk gets its final selection instead.
     auto process_batch = [&](int base, int count, bool final_pass) __attribute__((always_inline)) {
         const bool need = (lane < kQB) && (final_pass ? lane < nq : s_cnt[lane] > a.room - kBatch);
         unsigned long long m = __ballot(need);
@@ -316,7 +351,7 @@ void search_kernel(SearchArgs a) {
             }
             if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
         }
-        if (lane < count) {
+        if (!kTileExact && lane < count) {
             const int qn = s_qn[base + lane];
             const int pos = s_qpos[base + lane];
             const float e = exact_d2<DS, REV>(query_row(qn), a.pts + (size_t)pos * DS);
@@ -344,29 +379,35 @@ void search_kernel(SearchArgs a) {
 
     // Gather one tile of the stream into operand registers: the run lookup for
     // stream position v0 + n, the centred row half and the norm column.
+    // Packed shell key of a candidate row: segment * 2^21 + cell x (x < 2^20,
+    // segments < 32), 2^30 for rows past the tile.  A row is in the shell of
+    // a query with key k iff |key - k| <= 1 (same segment, x within one).
     struct Tile {
         float op[HD];
-        int pos, x, seg, count;
+        int pos, sx, count;
+        int idx;                        // original index (tile-exact path, h == 0 lanes)
     };
     auto gather = [&](int v0, int count, Tile& t) __attribute__((always_inline)) {
         const int v = v0 + n;
         const bool mvalid = n < count;
         t.count = count;
         t.pos = 0;
-        t.x = 0;
-        t.seg = -1;
+        t.sx = 1 << 30;
+        t.idx = -1;
         if (mvalid) {
             if (jr < ring_tail) jr = ring_tail;
             while (r_vend[jr & (kRing - 1)] <= v) ++jr;
             const int j = jr & (kRing - 1);
             t.pos = r_start[j] + (v - r_vbeg[j]);
-            t.x = r_x[j];
-            t.seg = r_seg[j];
+            t.sx = r_seg[j] * (1 << 21) + r_x[j];
+            if constexpr (kTileExact) {
+                if (h == 0) t.idx = BF ? t.pos : a.sorted_idx[t.pos];
+            }
         }
-        const float* fr = a.frows + (size_t)t.pos * DS + h * HD;
+        const float* pr = op_rows + (size_t)t.pos * DS + h * HD;
 #pragma unroll
         for (int j = 0; j < HD; j += 2) {
-            const float2 vv = *reinterpret_cast<const float2*>(fr + j);
+            const float2 vv = *reinterpret_cast<const float2*>(pr + j);
             t.op[j] = vv.x;
             t.op[j + 1] = vv.y;
         }
@@ -384,8 +425,9 @@ void search_kernel(SearchArgs a) {
         float pn = 0.0f;
 #pragma unroll
         for (int j = 0; j < HD; ++j) {
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(t.op[j], bop[j], acc, 0, 0, 0);
-            pn = fmaf(t.op[j], t.op[j], pn);
+            const float c = centre(t.op[j], j);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(c, bop[j], acc, 0, 0, 0);
+            pn = fmaf(c, c, pn);
         }
         const float nrm = pn + __shfl_xor(pn, 32);
         cand_norm = nrm;
@@ -393,13 +435,102 @@ void search_kernel(SearchArgs a) {
         return __builtin_amdgcn_mfma_f32_32x32x2f32(last, bop[HD], acc, 0, 0, 0);
     };
 
-    // Queue the tile's hits (filter value below the query's threshold, candidate
-    // inside the query's shell) for exact re-evaluation.
-    auto hits_tile = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
+    // Tile-exact path.  A hit is a pair with filter value below the query's
+    // threshold whose candidate lies in the query's shell: same row segment
+    // and cell x within one, i.e. packed keys seg * 2^21 + x within one (x <
+    // 2^20; rows past the tile carry 2^30).  The tile's raw rows go to LDS, each
+    // lane writes its hits after a wave prefix count, and the hits are
+    // re-evaluated in rounds of 64 lanes, each round preceded by the
+    // compaction of any list that could overflow during it.
+    auto hits_tile_exact = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
+        const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
+        unsigned fm = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const bool hit = robust ? !(acc[r] >= thr_f) : (acc[r] < thr_f);
+            fm |= (hit ? 1u : 0u) << r;
+        }
+        if (!qvalid) fm = 0;
+        if (__ballot(fm != 0) == 0) return;
+        lds_sync();
+        {
+            float* dst = t_rows + n * RS + h * HD;
+#pragma unroll
+            for (int j = 0; j < HD; ++j) dst[j] = t.op[j];
+            if (h == 0) {
+                t_idx[n] = t.idx;
+                t_sx[n] = t.sx;
+            }
+        }
+        lds_sync();
+        const int my_sx = BF ? 0 : my_seg * (1 << 21) + x_n;
+        unsigned mask = 0;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            if ((fm >> (4 * g4)) & 0xfu) {
+                const int4 sx = *reinterpret_cast<const int4*>(t_sx + 8 * g4 + 4 * h);
+                const int v4[4] = {sx.x, sx.y, sx.z, sx.w};
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const bool member = abs(v4[rr] - my_sx) <= 1;
+                    if (member) mask |= fm & (1u << (4 * g4 + rr));
+                }
+            }
+        }
+        const int cnt = __popc(mask);
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        const int total = __shfl(incl, kWave - 1);
+        if (total == 0) return;
+        int off = incl - cnt;
+        c_hit += cnt;
+        while (mask) {
+            const int r = __ffs(mask) - 1;
+            mask &= mask - 1;
+            const int row = 8 * (r >> 2) + 4 * h + (r & 3);
+            s_hit[off++] = (unsigned short)((row << 5) | n);
+        }
+        lds_sync();
+        for (int base = 0; base < total; base += kWave) {
+            const bool need = (lane < kQB) && s_cnt[lane] > a.room - kBatch;
+            unsigned long long m = __ballot(need);
+            if (m) {
+                while (m) {
+                    const int qn = __ffsll((long long)m) - 1;
+                    m &= m - 1;
+                    select_topk(qn, false);
+                }
+                if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
+            }
+            if (base + lane < total) {
+                const int e = s_hit[base + lane];
+                const int qn = e & 31;
+                const int row = e >> 5;
+                const float d2 = exact_d2<DS, REV>(s_q + qn * RS, t_rows + row * RS);
+                const unsigned long long key = make_key(d2, t_idx[row]);
+                if (key < s_thr[qn]) {
+                    const int slot = atomicAdd(&s_cnt[qn], 1);
+                    // compaction above leaves >= kBatch free slots; the guard
+                    // only keeps a logic error from writing past the list
+                    if (slot < a.room) lists[(size_t)qn * a.cap + slot] = key;
+                    else ++c_ovf;
+                    ++c_acc;
+                }
+            }
+            lds_sync();
+        }
+    };
+
+    // Queue path: queue the tile's hits (filter value below the query's
+    // threshold, candidate inside the query's shell) for exact re-evaluation.
+    auto hits_queue = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
         if (h == 0) {
             t_pos[n] = t.pos;
-            t_x[n] = t.x;
-            t_seg[n] = t.seg;
+            t_sx[n] = t.sx;
         }
         const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
         // per group of four accumulator registers: does this lane hold a hit?
@@ -432,9 +563,8 @@ void search_kernel(SearchArgs a) {
                     // 32x32 accumulator layout: lane (n, h), register r holds
                     // row 8*(r/4) + 4*h + r%4 (the candidate) of column n.
                     const int row = 8 * g4 + 4 * h + rr;
-                    const int tseg = t_seg[row];
-                    const bool member = BF ? (tseg >= 0)
-                                           : (tseg == my_seg && abs(t_x[row] - x_n) <= 1);
+                    const int my_sx = BF ? 0 : my_seg * (1 << 21) + x_n;
+                    const bool member = abs(t_sx[row] - my_sx) <= 1;
                     push = member && qvalid;
                     cpos = t_pos[row];
                 }
@@ -481,7 +611,8 @@ void search_kernel(SearchArgs a) {
             if constexpr (PREFETCH) {
                 if (has_next) gather(vn, min(32, an), nxt);
             }
-            hits_tile(cur, acc, cand_norm);
+            if constexpr (kTileExact) hits_tile_exact(cur, acc, cand_norm);
+            else hits_queue(cur, acc, cand_norm);
             if (h == 0 && n == 0) c_stream += cur.count;
             v_done = vn;
             while (ring_tail < ring_head && r_vend[ring_tail & (kRing - 1)] <= v_done) ++ring_tail;
@@ -783,7 +914,7 @@ static void launch_ds(const SearchArgs& a, bool bf, hipStream_t s) {
     else launch_one<DS, false, false>(a, s);
 }
 
-int launch_search(const float* aos, const float* frows, const float* fnorm, const int* sorted_idx,
+int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
                   const int* cell_of, const int* start, const void* frame_ws, int N, int D, int K,
                   const frnn_plan_t& plan, unsigned long long* lists, int cap, unsigned long long* counters,
                   hipStream_t s) {
@@ -791,11 +922,13 @@ int launch_search(const float* aos, const float* frows, const float* fnorm, cons
     const bool bf = plan.path == FRNN_PATH_BRUTEFORCE;
     if (!bf && (plan.grid_dim < 1 || plan.grid_dim > kMaxG || !sorted_idx || !cell_of || !start)) return 1;
     if (!bf && frame_ws && plan.grid_dim > kFrameGrid) return 1;
-    if (cap < list_capacity(K) || K > FRNN_MAX_K || !frows || !fnorm) return 1;
+    if (cap < list_capacity(K) || K > FRNN_MAX_K || !stats_ws || D < 1 || D > FRNN_MAX_DIM) return 1;
+    if (uses_filter_rows(D) && !frows) return 1;
     SearchArgs a{};
     a.pts = aos;
     a.frows = frows;
-    a.fnorm = fnorm;
+    a.st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
+    a.D = D;
     a.sorted_idx = sorted_idx;
     a.cell_of = cell_of;
     a.start = start;

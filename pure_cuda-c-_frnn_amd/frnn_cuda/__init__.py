@@ -123,8 +123,9 @@ def _load():
         "frnn_frame_workspace_bytes": ([i32, i32, ctypes.POINTER(_Plan)], i64),
         "frnn_launch_frame": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp], i32),
         "frnn_launch_refine": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp, vp, vp], i32),
-        "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, vp], i32),
-        "frnn_launch_transpose": ([vp, i32, i32, vp, vp, vp, vp, vp], i32),
+        "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
+        "frnn_launch_transpose": ([vp, i32, i32, vp, vp, vp, vp], i32),
+        "frnn_uses_filter_rows": ([i32], i32),
         "frnn_launch_find_nbrs": ([vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan),
                                    vp, i32, vp, vp], i32),
         "frnn_launch_unpermute": ([vp, i32, vp, i32, i32, vp, vp, vp], i32),

@@ -41,7 +41,7 @@ def _build(X, g, res, inv):
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.full((N * ds,), float("nan"), dtype=t.float32, device="cuda:0")
     assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), None, cells,
-                                 vp(sidx), vp(inv_p), vp(aos), None, None, None, None) == 0
+                                 vp(sidx), vp(inv_p), vp(aos), None, None, None) == 0
     t.cuda.synchronize()
     return {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start,
                                                   sidx=sidx, inv=inv_p, aos=aos).items()}
@@ -159,12 +159,11 @@ def _frame_build(X, K, radius):
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
     frows = t.empty(N * ds, dtype=t.float32, device="cuda:0")
-    fnorm = t.empty(N, dtype=t.float32, device="cuda:0")
     assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
-                                 vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), vp(fnorm), None) == 0
+                                 vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), None) == 0
     t.cuda.synchronize()
     out = {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start, sidx=sidx,
-                                                 inv=inv_p, aos=aos, frows=frows, fnorm=fnorm).items()}
+                                                 inv=inv_p, aos=aos, frows=frows).items()}
     out["frame"] = frnn_cuda.FrameInfo.from_workspace(ws[:4096].cpu().numpy())
     out["stats"] = sws[:16 * D].cpu().numpy().view(np.float32).reshape(D, 4)
     out["plan"], out["cells"] = plan, cells
@@ -269,10 +268,10 @@ def test_frame_grid_and_refinement(name, N):
     assert np.all(np.diff(cs) >= 0)
     ds = frnn_cuda.aos_stride(w.D)
     assert np.array_equal(out["aos"].reshape(N, ds)[:, :w.D], w.X[sidx])
+    # centred filter rows: fl(x - mean), zero padded
     fr = out["frows"].reshape(N, ds)
     assert np.array_equal(fr[:, :w.D], (w.X[sidx] - mean[None, :]).astype(np.float32))
     assert np.all(fr[:, w.D:] == 0)
-    assert np.array_equal(out["fnorm"], E.dist2(fr, np.zeros_like(fr), 0))
     # sub-bin order inside cells holding >= 256 points
     r0, r1 = S[g], S[g + 1] if fi.axes > 1 else np.zeros(N, np.float32)
     key = _sub_bins(r0[sidx], fi.rlo0, fi.rinv0, fi.bins0) * fi.bins1
@@ -357,13 +356,12 @@ def test_seam_search_first_coordinate_plan(framed):
     sidx = t.empty(N, dtype=t.int32, device="cuda:0")
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
-    frows = t.empty(N * ds, dtype=t.float32, device="cuda:0")
-    fnorm = t.empty(N, dtype=t.float32, device="cuda:0")
+    assert L.frnn_uses_filter_rows(D) == 0
     assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
-                                 vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), vp(fnorm), None) == 0
+                                 vp(sidx), vp(inv_p), vp(aos), None, None, None) == 0
     cap = frnn_cuda.list_capacity(K)
     lists = t.empty(N * cap, dtype=t.int64, device="cuda:0")
-    assert L.frnn_launch_find_nbrs(vp(aos), vp(frows), vp(fnorm), vp(sidx), vp(cell_of), vp(start), vp(ws),
+    assert L.frnn_launch_find_nbrs(vp(aos), None, vp(sws), vp(sidx), vp(cell_of), vp(start), vp(ws),
                                    N, D, K, ctypes.byref(plan), vp(lists), cap, None, None) == 0
     idx = t.empty(K * N, dtype=t.int32, device="cuda:0")
     dist = t.empty(K * N, dtype=t.float32, device="cuda:0")
