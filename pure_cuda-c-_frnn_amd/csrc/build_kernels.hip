@@ -171,8 +171,7 @@ __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ 
     const int c = cell_of[i];
     int pos = start[c] + rank[i];
     if (subkey && cnt[c] >= kBigCell) {
-        const size_t base = (size_t)bidx[c] * kSubBins;
-        pos += substart[base + subkey[i]] - substart[base];
+        pos += substart[(size_t)bidx[c] * kSubStride + subkey[i]];
     }
     sorted_idx[pos] = i;
     inv[i] = pos;
@@ -411,9 +410,10 @@ constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 
 // Principal directions and geometry of a frame (fp64, one wave; lane t holds
 // component t of every direction).  The m = g + L leading eigenvectors of the
-// sampled covariance come from 16 steps of subspace iteration (modified
-// Gram-Schmidt, iterates broadcast through LDS) and a final Rayleigh-Ritz step
-// (cyclic Jacobi on the m x m projected matrix, in registers).  Directions 0..g-1 become the grid axes, the next L the refinement
+// sampled covariance C come from subspace iteration on (C / cmax)^4 (two
+// squarings in LDS, then 4 steps: 16 steps' worth on C; modified
+// Gram-Schmidt) and a final Rayleigh-Ritz step on C (cyclic Jacobi on the
+// m x m projected matrix, in registers).  Directions 0..g-1 become the grid axes, the next L the refinement
 // directions (slots 4, 5); weights are scaled by 1 - 2^-18, so the fp32 grid
 // directions stay orthonormal up to a shrink (|U d| <= |d| for any d) and
 // every direction has norm < 1.
@@ -430,19 +430,19 @@ constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict__ covsum, double nsamp,
                                                         float radius, float cell_raw, float inv_cell_raw,
                                                         int res_raw, int cells_cap, Frame* __restrict__ f) {
-    __shared__ double s_C[kMaxTerms][kMaxTerms + 1];
+    __shared__ double s_C[kMaxTerms][kMaxTerms + 1];   // covariance
+    __shared__ double s_A[kMaxTerms][kMaxTerms + 1];   // (C / cmax)^2
+    __shared__ double s_P[kMaxTerms][kMaxTerms + 1];   // C / cmax, then (C / cmax)^4
     __shared__ double s_v[kMaxDirs][kMaxTerms];
     const int t = threadIdx.x;
     const int T = f->terms;
     const int g = f->g;
     const int m = g + f->L;
     const int P = T * (T + 1) / 2;
-    for (int p = t; p < P; p += kWave) {
-        int a, c;
-        pair_of(p, T, a, c);
-        const double v = covsum[p] / nsamp;
-        s_C[a][c] = v;
-        s_C[c][a] = v;
+    for (int i = t; i < kMaxTerms * (kMaxTerms + 1); i += kWave) {
+        (&s_C[0][0])[i] = 0.0;
+        (&s_A[0][0])[i] = 0.0;
+        (&s_P[0][0])[i] = 0.0;
     }
     const bool on = t < T;
     auto lds_fence = [&]() {
@@ -451,6 +451,43 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
     lds_fence();
+    for (int p = t; p < P; p += kWave) {
+        int a, c;
+        pair_of(p, T, a, c);
+        const double v = covsum[p] / nsamp;
+        s_C[a][c] = v;
+        s_C[c][a] = v;
+    }
+    lds_fence();
+    // The iteration runs on (C / cmax)^4 (cmax the largest diagonal entry, so
+    // the powers stay in range): one step there is four steps on C.  Row t of
+    // a product is formed by lane t.
+    double cmax = 0.0;
+    for (int k = 0; k < T; ++k) cmax = fmax(cmax, s_C[k][k]);
+    const double cs = (cmax > 0.0 && cmax < 1.0e300) ? 1.0 / cmax : 1.0;
+    if (on)
+        for (int k = 0; k < kMaxTerms; ++k) s_P[t][k] = s_C[t][k] * cs;
+    lds_fence();
+    auto square = [&](double (*src)[kMaxTerms + 1], double (*dst)[kMaxTerms + 1]) {
+        double acc[kMaxTerms];
+#pragma unroll
+        for (int k = 0; k < kMaxTerms; ++k) acc[k] = 0.0;
+        if (on) {
+            for (int l = 0; l < T; ++l) {
+                const double a = src[t][l];
+#pragma unroll
+                for (int k = 0; k < kMaxTerms; ++k) acc[k] = fma(a, src[l][k], acc[k]);
+            }
+        }
+        lds_fence();
+        if (on) {
+#pragma unroll
+            for (int k = 0; k < kMaxTerms; ++k) dst[t][k] = (k < T) ? acc[k] : 0.0;
+        }
+        lds_fence();
+    };
+    square(s_P, s_A);
+    square(s_A, s_P);
     double v[kMaxDirs];
 #pragma unroll
     for (int j = 0; j < kMaxDirs; ++j)
@@ -483,8 +520,9 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
             v[j] /= nrm;
         }
     };
-    // w_j = C v_j for all directions, from one LDS broadcast of the iterate
-    auto matvec = [&](double (&w)[kMaxDirs]) {
+    // w_j = M v_j for all directions (M = C or its scaled fourth power), from
+    // one LDS broadcast of the iterate
+    auto matvec = [&](double (*M)[kMaxTerms + 1], double (&w)[kMaxDirs]) {
 #pragma unroll
         for (int j = 0; j < kMaxDirs; ++j)
             if (on && j < m) s_v[j][t] = v[j];
@@ -492,7 +530,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
 #pragma unroll
         for (int j = 0; j < kMaxDirs; ++j) w[j] = 0.0;
         for (int k = 0; k < T; ++k) {
-            const double c = s_C[on ? t : 0][k];
+            const double c = M[on ? t : 0][k];
 #pragma unroll
             for (int j = 0; j < kMaxDirs; ++j)
                 if (j < m) w[j] = fma(c, s_v[j][k], w[j]);
@@ -503,9 +541,9 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
             if (!on) w[j] = 0.0;
     };
     orthonormalise();
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < 4; ++it) {
         double w[kMaxDirs];
-        matvec(w);
+        matvec(s_P, w);
 #pragma unroll
         for (int j = 0; j < kMaxDirs; ++j) v[j] = w[j];
         orthonormalise();
@@ -516,7 +554,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     double H[kMaxDirs][kMaxDirs], R[kMaxDirs][kMaxDirs];
     {
         double w[kMaxDirs];
-        matvec(w);
+        matvec(s_C, w);
 #pragma unroll
         for (int j = 0; j < kMaxDirs; ++j)
 #pragma unroll
@@ -533,7 +571,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
             H[j][k] = sym;
             H[k][j] = sym;
         }
-    for (int sweep = 0; sweep < 30; ++sweep) {
+    for (int sweep = 0; sweep < 20; ++sweep) {
         double off = 0.0, dia = 0.0;
 #pragma unroll
         for (int j = 0; j < kMaxDirs; ++j) {
@@ -724,6 +762,50 @@ __global__ __launch_bounds__(256) void sub_count_kernel(const float* __restrict_
     rank[i] = atomicAdd(&subcnt[(size_t)bidx[c] * kSubBins + key], 1);
 }
 
+// Sub-bin tables of the big cells: block b (one per possible big cell) clears
+// (zero_sub_kernel) or exclusively scans (sub_scan_kernel, 1025 entries, the
+// last the cell's total) the 1024 sub-bin counts of big cell b; blocks past
+// the number of big cells (bidx[cells]) exit at once.
+__global__ __launch_bounds__(256) void zero_sub_kernel(const int* __restrict__ bidx, long long cells,
+                                                       int* __restrict__ subcnt) {
+    if ((int)blockIdx.x >= bidx[cells]) return;
+    int* row = subcnt + (size_t)blockIdx.x * kSubBins;
+    for (int k = threadIdx.x; k < kSubBins; k += blockDim.x) row[k] = 0;
+}
+
+__global__ __launch_bounds__(256) void sub_scan_kernel(const int* __restrict__ bidx, long long cells,
+                                                       const int* __restrict__ subcnt,
+                                                       int* __restrict__ substart) {
+    constexpr int kPer = kSubBins / 256;
+    __shared__ int s_part[256];
+    if ((int)blockIdx.x >= bidx[cells]) return;
+    const int tid = threadIdx.x;
+    const int* row = subcnt + (size_t)blockIdx.x * kSubBins;
+    int v[kPer];
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        v[j] = row[tid * kPer + j];
+        sum += v[j];
+    }
+    s_part[tid] = sum;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {   // inclusive scan of the per-thread sums
+        const int y = tid >= o ? s_part[tid - o] : 0;
+        __syncthreads();
+        s_part[tid] += y;
+        __syncthreads();
+    }
+    int run = s_part[tid] - sum;
+    int* out = substart + (size_t)blockIdx.x * kSubStride;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        out[tid * kPer + j] = run;
+        run += v[j];
+    }
+    if (tid == 255) out[kSubBins] = run;
+}
+
 __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ pts, int N, int D, int ds,
                                                         float* __restrict__ aos,
                                                         const DimStat* __restrict__ st,
@@ -733,33 +815,53 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict_
     write_row(pts, N, D, ds, i, i, aos, st, frows);
 }
 
-// Output transpose through LDS, 32 original queries per workgroup: the K keys
-// of each query's list (row inv[i] of the sorted order) are read with
-// consecutive threads on consecutive keys, then each k writes the 32 queries'
-// index and distance as one contiguous 128-byte segment of the SoA outputs.
-constexpr int kUnpermQ = 32;
+// Output transpose through LDS, qt original queries per workgroup (64, or 32
+// for K > 64): each query's K keys (row inv[i] of the sorted order,
+// contiguous) are read as 16-byte pairs and split into index and distance
+// columns of two padded LDS tiles [k][query]; then the workgroup writes whole
+// output rows k, qt consecutive queries per store.
+// The two tiles take 2 * K * (qt + 1) * 4 bytes of dynamic LDS; pairs is set
+// when K and cap are even and lists is 16-byte aligned.
 __global__ __launch_bounds__(256) void unpermute_kernel(const unsigned long long* __restrict__ lists,
                                                         int cap, const int* __restrict__ inv, int N,
-                                                        int K, int* __restrict__ idxs,
+                                                        int K, int qt, int pairs, int* __restrict__ idxs,
                                                         float* __restrict__ dists) {
-    __shared__ unsigned long long s_t[kUnpermQ * (FRNN_MAX_K + 1)];
-    const int i0 = blockIdx.x * kUnpermQ;
-    const int nq = min(kUnpermQ, N - i0);
-    const int stride = K + 1;
-    for (int j = threadIdx.x; j < nq * K; j += blockDim.x) {
-        const int q = j / K;
-        const int k = j - q * K;
-        const int sp = inv ? inv[i0 + q] : i0 + q;
-        s_t[q * stride + k] = lists[(size_t)sp * cap + k];
+    const int kPitch = qt + 1;
+    extern __shared__ int s_dyn[];
+    int* const s_idx = s_dyn;
+    float* const s_d2 = reinterpret_cast<float*>(s_dyn + K * kPitch);
+    const int i0 = blockIdx.x * qt;
+    const int nq = min(qt, N - i0);
+    const int tid = threadIdx.x;
+    if (pairs) {
+        const int half = K >> 1;   // key pairs per query
+        for (int j = tid; j < nq * half; j += blockDim.x) {
+            const int q = j / half;
+            const int k = 2 * (j - q * half);
+            const int sp = inv ? inv[i0 + q] : i0 + q;
+            const ulonglong2 kv = *reinterpret_cast<const ulonglong2*>(lists + (size_t)sp * cap + k);
+            s_idx[k * kPitch + q] = (int)(unsigned int)kv.x;
+            s_d2[k * kPitch + q] = key_d2(kv.x);
+            s_idx[(k + 1) * kPitch + q] = (int)(unsigned int)kv.y;
+            s_d2[(k + 1) * kPitch + q] = key_d2(kv.y);
+        }
+    } else {
+        for (int j = tid; j < nq * K; j += blockDim.x) {
+            const int q = j / K;
+            const int k = j - q * K;
+            const int sp = inv ? inv[i0 + q] : i0 + q;
+            const unsigned long long key = lists[(size_t)sp * cap + k];
+            s_idx[k * kPitch + q] = (int)(unsigned int)key;
+            s_d2[k * kPitch + q] = key_d2(key);
+        }
     }
     __syncthreads();
-    for (int j = threadIdx.x; j < K * kUnpermQ; j += blockDim.x) {
-        const int k = j / kUnpermQ;
-        const int q = j - k * kUnpermQ;
+    for (int j = tid; j < K * qt; j += blockDim.x) {
+        const int k = j / qt;
+        const int q = j - k * qt;
         if (q < nq) {
-            const unsigned long long key = s_t[q * stride + k];
-            idxs[(size_t)k * N + i0 + q] = (int)(unsigned int)key;
-            dists[(size_t)k * N + i0 + q] = key_d2(key);
+            idxs[(size_t)k * N + i0 + q] = s_idx[k * kPitch + q];
+            dists[(size_t)k * N + i0 + q] = s_d2[k * kPitch + q];
         }
     }
 }
@@ -817,13 +919,12 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 FrameLayout frame_layout(int N, int D, long long cells) {
     FrameLayout L{};
     L.max_big = N / kBigCell;
-    L.nsub = L.max_big * kSubBins + 1;
     size_t off = 0;
     L.frame = off;    off = align256(off + sizeof(Frame));
     L.bidx = off;     off = align256(off + (size_t)(cells + 1) * sizeof(int));
-    L.subcnt = off;   off = align256(off + (size_t)L.nsub * sizeof(int));
-    L.substart = off; off = align256(off + (size_t)L.nsub * sizeof(int));
-    const int np = scan_partials_count(L.nsub > cells + 1 ? L.nsub : (int)(cells + 1));
+    L.subcnt = off;   off = align256(off + (size_t)L.max_big * kSubBins * sizeof(int));
+    L.substart = off; off = align256(off + (size_t)L.max_big * kSubStride * sizeof(int));
+    const int np = scan_partials_count((int)(cells + 1));
     L.scanpart = off; off = align256(off + (size_t)np * sizeof(int));
     L.cov = off;      off = align256(off + (size_t)kCovBlocks * kMaxPairs * sizeof(double));
     L.covsum = off;   off = align256(off + (size_t)kMaxPairs * sizeof(double));
@@ -887,14 +988,13 @@ int launch_refine(const float* pts, int N, int D, long long cells, const int* ce
     int* substart = reinterpret_cast<int*>(base + L.substart);
     int* scanpart = reinterpret_cast<int*>(base + L.scanpart);
     int* subkey = reinterpret_cast<int*>(base + L.subkey);
-    int rc = launch_exclusive_scan(cnt, (int)cells + 1, bidx, scanpart, s, kBigCell);
+    const int rc = launch_exclusive_scan(cnt, (int)cells + 1, bidx, scanpart, s, kBigCell);
     if (rc) return rc;
-    rc = launch_fill_i32(subcnt, L.nsub, 0, s);
-    if (rc) return rc;
+    if (L.max_big == 0) return launch_result();   // no cell can hold kBigCell points
+    hipLaunchKernelGGL(zero_sub_kernel, dim3(L.max_big), dim3(256), 0, s, bidx, cells, subcnt);
     hipLaunchKernelGGL(sub_count_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, cell_of, cnt,
                        bidx, f, subcnt, rank, subkey);
-    rc = launch_exclusive_scan(subcnt, L.nsub, substart, scanpart, s);
-    if (rc) return rc;
+    hipLaunchKernelGGL(sub_scan_kernel, dim3(L.max_big), dim3(256), 0, s, bidx, cells, subcnt, substart);
     return launch_result();
 }
 
@@ -937,8 +1037,11 @@ int launch_unpermute(const unsigned long long* lists, int cap, const int* inv, i
                      float* dists, hipStream_t s) {
     if (N <= 0) return 0;
     if (K < 1 || K > FRNN_MAX_K || cap < K) return 1;   // the LDS tile holds K <= FRNN_MAX_K keys
-    hipLaunchKernelGGL(unpermute_kernel, dim3(blocks_for(N, kUnpermQ)), dim3(256), 0, s, lists, cap, inv, N,
-                       K, idxs, dists);
+    const int pairs = (K % 2 == 0 && cap % 2 == 0 && (reinterpret_cast<uintptr_t>(lists) & 15) == 0) ? 1 : 0;
+    const int qt = K > 64 ? 32 : 64;
+    const size_t lds = (size_t)2 * K * (qt + 1) * sizeof(int);   // <= 33 KiB
+    hipLaunchKernelGGL(unpermute_kernel, dim3(blocks_for(N, qt)), dim3(256), lds, s, lists, cap, inv, N,
+                       K, qt, pairs, idxs, dists);
     return launch_result();
 }
 

@@ -29,6 +29,7 @@ int scan_partials_count(int n);
 // its queries' windows.
 constexpr int kBigCell = 256;
 constexpr int kSubBins = 1024;
+constexpr int kSubStride = kSubBins + 1;   // per big cell: sub-bin offsets and the cell total
 constexpr int kStatBlocks = 64;        // point slices per coordinate (statistics)
 constexpr int kMaxTerms = FRNN_FRAME_TERMS;
 constexpr int kMaxPairs = kMaxTerms * (kMaxTerms + 1) / 2;   // covariance entries
@@ -56,7 +57,6 @@ static_assert(sizeof(Frame) == sizeof(frnn_frame_t), "Frame mirrors frnn_frame_t
 struct FrameLayout {
     size_t frame, bidx, subcnt, substart, scanpart, cov, covsum, subkey, total;   // byte offsets
     int max_big;        // upper bound on cells with >= kBigCell points
-    int nsub;           // max_big * kSubBins + 1 scanned entries
 };
 
 // Per-coordinate statistics of the input (fp64 accumulation): the mean is the

@@ -69,7 +69,7 @@ struct SearchArgs {
     const int* start;            // cells+1 exclusive cell offsets (grid paths)
     const Frame* frame;          // first-coordinate grid frame, or nullptr (raw grid)
     const int* bidx;             // big-cell index (exclusive scan of big flags)
-    const int* substart;         // sub-bin offsets of big cells
+    const int* substart;         // sub-bin offsets within each big cell (kSubStride per cell)
     unsigned long long* lists;   // [N][cap] candidate keys
     unsigned long long* counters;
     int N, D, K, cap, G, res;    // res: raw-grid cells per axis
@@ -856,11 +856,10 @@ void search_kernel(SearchArgs a) {
                     if (c_runs > 1 || (windowed && c_end - c_start >= kBigCell)) {
                         // sub-bin row qlo0 + kk of the window, columns qlo1..qhi1
                         const int q1 = qlo0 + kk;
-                        const size_t sb = (size_t)a.bidx[c_cell] * kSubBins;
-                        const int s0 = a.substart[sb];
+                        const size_t sb = (size_t)a.bidx[c_cell] * kSubStride;
                         const int sl = a.substart[sb + q1 * nb2 + qlo1];
                         const int sh = a.substart[sb + q1 * nb2 + qhi1 + 1];
-                        rs = c_start + (sl - s0);
+                        rs = c_start + sl;
                         rl = sh - sl;
                     } else {
                         rs = c_start;
