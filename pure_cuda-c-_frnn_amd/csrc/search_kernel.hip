@@ -8,12 +8,11 @@
 // Work decomposition (one 64-lane wave per workgroup):
 //   * a wave owns 32 consecutive queries of the cell-sorted order (grid paths)
 //     or of the original order (brute force);
-//   * for grid paths the wave walks, for each run of its queries' rows, the
-//     3^(g-1) neighbouring rows; in each neighbouring row the cells x-1..x+1 of
-//     one query are a contiguous span of the sorted points, so the union over
-//     the wave is one contiguous candidate range per neighbouring row.  Each
-//     query only accepts candidates inside its own 3^g shell ([lo, hi) per row),
-//     with conservative AABB trimming of the outer x cells;
+//   * for grid paths the wave walks, for each run of its queries sharing a
+//     row (the cells of equal coordinates on axes 1..g-1), the cells x-1..x+1
+//     around the run's queries in the 3^(g-1) neighbouring rows, skipping
+//     cells whose box is farther than every query's threshold (and, inside
+//     refined big cells, sub-bins outside the run's projection window);
 //   * candidates stream through in tiles of 32.  The distance tile
 //     32 candidates x 32 queries is one chain of v_mfma_f32_32x32x2f32 on the
 //     augmented vectors  a = [p', |p'|^2, 1],  b = [-2q', 1-c, (1-c)|q'|^2]
@@ -21,9 +20,12 @@
 //     their squared norms), so the accumulator is a filter value F <= the
 //     exact distance plus a proven rounding bound;
 //   * pairs with F below the query's threshold (plus a relative margin) are
-//     queued in LDS and re-evaluated 64 at a time with the reference's exact fp32
-//     distance order on the raw rows (the lines the filter just gathered);
-//     accepted (d2, idx) keys go to a per-query candidate list;
+//     re-evaluated with the reference's exact fp32 distance order: right after
+//     the tile from its raw rows staged in LDS (rows up to 32 floats), or
+//     queued and re-evaluated 64 at a time from memory (wider rows); accepted
+//     (d2, idx) keys go to a per-query candidate list.  Every pair within the
+//     radius lies in the query's shell, so candidates streamed for other
+//     queries of the wave need no membership test: they fail the exact test;
 //   * when a list nears capacity the wave sorts it cooperatively (bitonic in
 //     registers, up to 4 keys per lane), keeps the K smallest and tightens the
 //     query's threshold to the K-th key; at the end every list is sorted and its
@@ -149,14 +151,13 @@ void search_kernel(SearchArgs a) {
     constexpr bool kTileExact = DS <= 32;
     __shared__ unsigned char s_qn[kTileExact ? 1 : kQueueCap];
     __shared__ int s_qpos[kTileExact ? 1 : kQueueCap];
-    // candidate run ring: [start, start + (vend - vbeg)) of the sorted points,
-    // virtual stream positions [vbeg, vend), cell x and row-segment id
-    __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing], r_x[kRing], r_seg[kRing];
-    // current tile, per candidate row: the packed (segment, cell x) shell key
-    // and the original index (tile-exact path) or sorted position (queue
-    // path); tile-exact path: the raw rows (stride RS, as s_q) and the hit
-    // entries (row << 5 | query)
-    __shared__ int t_idx[32], t_sx[32];
+    // candidate run ring: [start, start + (vend - vbeg)) of the sorted points
+    // at virtual stream positions [vbeg, vend)
+    __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing];
+    // current tile, per candidate row: the original index (tile-exact path)
+    // or sorted position (queue path); tile-exact path: the raw rows (stride
+    // RS, as s_q) and the hit entries (row << 5 | query)
+    __shared__ int t_idx[32];
     __shared__ int t_pos[kTileExact ? 1 : 32];
     __shared__ __align__(16) float t_rows[kTileExact ? 32 * RS : 4];
     __shared__ unsigned short s_hit[kTileExact ? 32 * 32 : 2];
@@ -374,32 +375,31 @@ void search_kernel(SearchArgs a) {
     int ring_head = 0, ring_tail = 0;   // absolute run indices (wave-uniform)
     int v_total = 0, v_done = 0;        // virtual candidate positions (wave-uniform)
     int jr = 0;                         // this lane's current run
-    int my_seg = -1;                    // row segment of this lane's query
     int x_n = 0;                        // cell x of this lane's query
+    // stream positions of the candidates streamed for this lane's query's
+    // row segment (the segment still streaming ends at INT_MAX)
+    int q_vbeg = 0, q_vend = 0;
 
     // Gather one tile of the stream into operand registers: the run lookup for
     // stream position v0 + n, the centred row half and the norm column.
-    // Packed shell key of a candidate row: segment * 2^21 + cell x (x < 2^20,
-    // segments < 32), 2^30 for rows past the tile.  A row is in the shell of
-    // a query with key k iff |key - k| <= 1 (same segment, x within one).
     struct Tile {
         float op[HD];
-        int pos, sx, count;
+        int pos, count;
+        int v0;                         // stream position of row 0
         int idx;                        // original index (tile-exact path, h == 0 lanes)
     };
     auto gather = [&](int v0, int count, Tile& t) __attribute__((always_inline)) {
         const int v = v0 + n;
         const bool mvalid = n < count;
         t.count = count;
+        t.v0 = v0;
         t.pos = 0;
-        t.sx = 1 << 30;
         t.idx = -1;
         if (mvalid) {
             if (jr < ring_tail) jr = ring_tail;
             while (r_vend[jr & (kRing - 1)] <= v) ++jr;
             const int j = jr & (kRing - 1);
             t.pos = r_start[j] + (v - r_vbeg[j]);
-            t.sx = r_seg[j] * (1 << 21) + r_x[j];
             if constexpr (kTileExact) {
                 if (h == 0) t.idx = BF ? t.pos : a.sorted_idx[t.pos];
             }
@@ -435,65 +435,74 @@ void search_kernel(SearchArgs a) {
         return __builtin_amdgcn_mfma_f32_32x32x2f32(last, bop[HD], acc, 0, 0, 0);
     };
 
-    // Tile-exact path.  A hit is a pair with filter value below the query's
-    // threshold whose candidate lies in the query's shell: same row segment
-    // and cell x within one, i.e. packed keys seg * 2^21 + x within one (x <
-    // 2^20; rows past the tile carry 2^30).  The tile's raw rows go to LDS, each
-    // lane writes its hits after a wave prefix count, and the hits are
-    // re-evaluated in rounds of 64 lanes, each round preceded by the
-    // compaction of any list that could overflow during it.
+    // A hit is a pair (candidate row, query) whose filter value is below the
+    // query's threshold (NaN counts as a hit) and whose candidate was streamed
+    // for the query's own row segment: stream positions [q_vbeg, q_vend) of
+    // this lane's query (empty for invalid queries), clipped to the tile's
+    // rows.  That keeps each candidate to one evaluation per query (the
+    // neighbourhoods of a wave's segments overlap).  Inside its segment's
+    // stream a candidate needs no finer shell test: every pair within the
+    // radius lies in the query's 3^g shell (the grid's cell edge covers the
+    // radius plus all rounding), so other candidates fail the exact test, and
+    // the filter passes them only within its margin of the radius.
+    //
+    // The 32 x 32 accumulator layout: lane (n, h), register r holds row
+    // 8*(r/4) + 4*h + r%4 (the candidate) of column n.  For a tile at stream
+    // position v0, rows_of returns this lane's accepted range of rowlo =
+    // 8*(r/4) + r%4 as (first, width); hit_in tests register r.
+    auto rows_of = [&](int v0, int count, int& first, int& width) __attribute__((always_inline)) {
+        const int lo = max(q_vbeg - v0, 0);
+        const int hi = min(q_vend - v0, count);
+        first = lo - 4 * h;
+        width = max(hi - lo, 0);
+    };
+    auto hit_in = [&](const floatx16& acc, int r, int first, int width) __attribute__((always_inline)) {
+        const int rowlo = 8 * (r >> 2) + (r & 3);
+        return !(acc[r] >= thr_f) && (unsigned)(rowlo - first) < (unsigned)width;
+    };
+    // whether any lane's filter values might hold a hit (a cheap first test:
+    // the smallest of the 16 values, or always when NaN may occur)
+    auto any_hit = [&](const floatx16& acc, bool robust) __attribute__((always_inline)) {
+        if (robust) return true;
+        float mn = acc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mn = fminf(mn, acc[r]);
+        return __ballot(qvalid && mn < thr_f) != 0;
+    };
+
+    // Tile-exact path: the tile's raw rows and original indices go to LDS,
+    // the hits (row << 5 | query) are written register by register at ballot
+    // prefix offsets, and they are re-evaluated in rounds of 64 lanes, each
+    // round preceded by the compaction of any list that could overflow in it.
     auto hits_tile_exact = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
         const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
-        unsigned fm = 0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const bool hit = robust ? !(acc[r] >= thr_f) : (acc[r] < thr_f);
-            fm |= (hit ? 1u : 0u) << r;
-        }
-        if (!qvalid) fm = 0;
-        if (__ballot(fm != 0) == 0) return;
+        if (!any_hit(acc, robust)) return;
         lds_sync();
         {
             float* dst = t_rows + n * RS + h * HD;
 #pragma unroll
             for (int j = 0; j < HD; ++j) dst[j] = t.op[j];
-            if (h == 0) {
-                t_idx[n] = t.idx;
-                t_sx[n] = t.sx;
-            }
+            if (h == 0) t_idx[n] = t.idx;
         }
-        lds_sync();
-        const int my_sx = BF ? 0 : my_seg * (1 << 21) + x_n;
-        unsigned mask = 0;
+        const int lane_code = (h << 7) | n;   // (4h << 5) | n
+        int first, width;
+        rows_of(t.v0, t.count, first, width);
+        int total = 0;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-            if ((fm >> (4 * g4)) & 0xfu) {
-                const int4 sx = *reinterpret_cast<const int4*>(t_sx + 8 * g4 + 4 * h);
-                const int v4[4] = {sx.x, sx.y, sx.z, sx.w};
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const bool member = abs(v4[rr] - my_sx) <= 1;
-                    if (member) mask |= fm & (1u << (4 * g4 + rr));
+        for (int r = 0; r < 16; ++r) {
+            const bool hr = hit_in(acc, r, first, width);
+            const unsigned long long m = __ballot(hr);
+            if (m) {
+                if (hr) {
+                    const int off = total + (int)__builtin_amdgcn_mbcnt_hi(
+                                                (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+                    s_hit[off] = (unsigned short)(((8 * (r >> 2) + (r & 3)) << 5) + lane_code);
+                    ++c_hit;
                 }
+                total += __popcll(m);
             }
         }
-        const int cnt = __popc(mask);
-        int incl = cnt;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int y = __shfl_up(incl, o);
-            if (lane >= o) incl += y;
-        }
-        const int total = __shfl(incl, kWave - 1);
         if (total == 0) return;
-        int off = incl - cnt;
-        c_hit += cnt;
-        while (mask) {
-            const int r = __ffs(mask) - 1;
-            mask &= mask - 1;
-            const int row = 8 * (r >> 2) + 4 * h + (r & 3);
-            s_hit[off++] = (unsigned short)((row << 5) | n);
-        }
         lds_sync();
         for (int base = 0; base < total; base += kWave) {
             const bool need = (lane < kQB) && s_cnt[lane] > a.room - kBatch;
@@ -525,63 +534,53 @@ void search_kernel(SearchArgs a) {
         }
     };
 
-    // Queue path: queue the tile's hits (filter value below the query's
-    // threshold, candidate inside the query's shell) for exact re-evaluation.
+    // Queue path: the tile's hits are queued as (query, sorted position) and
+    // re-evaluated 64 at a time from memory.  All hits of the tile are queued
+    // first (at most 1024, so the queue never exceeds 63 + 1024 entries); the
+    // exact batches run after, when the accumulator registers are no longer
+    // live.
     auto hits_queue = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
-        if (h == 0) {
-            t_pos[n] = t.pos;
-            t_sx[n] = t.sx;
-        }
         const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
-        // per group of four accumulator registers: does this lane hold a hit?
+        // hits are sparse here: first find the groups of four registers that
+        // might hold one
         bool gh[4];
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
             if (!robust) {
                 const float m = fminf(fminf(acc[4 * g4], acc[4 * g4 + 1]), fminf(acc[4 * g4 + 2], acc[4 * g4 + 3]));
-                gh[g4] = m < thr_f;
+                gh[g4] = qvalid && m < thr_f;
             } else {
-                gh[g4] = !(acc[4 * g4] >= thr_f) || !(acc[4 * g4 + 1] >= thr_f) ||
-                         !(acc[4 * g4 + 2] >= thr_f) || !(acc[4 * g4 + 3] >= thr_f);
+                gh[g4] = qvalid;
             }
         }
         if (__ballot(gh[0] || gh[1] || gh[2] || gh[3]) == 0) return;
         lds_sync();
-        // All hits of the tile are queued first (at most 16 per lane, so the
-        // queue never exceeds 63 + 1024 entries); the exact batches run after,
-        // when the accumulator registers are no longer live.  Queue slots come
-        // from a ballot prefix count, so pushes need no atomics.
+        if (h == 0) t_pos[n] = t.pos;
+        lds_sync();
+        int first, width;
+        rows_of(t.v0, t.count, first, width);
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
             if (__ballot(gh[g4]) == 0) continue;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int r = 4 * g4 + rr;
-                bool push = false;
-                int cpos = 0;
-                if (gh[g4] && !(acc[r] >= thr_f)) {
-                    // 32x32 accumulator layout: lane (n, h), register r holds
-                    // row 8*(r/4) + 4*h + r%4 (the candidate) of column n.
-                    const int row = 8 * g4 + 4 * h + rr;
-                    const int my_sx = BF ? 0 : my_seg * (1 << 21) + x_n;
-                    const bool member = abs(t_sx[row] - my_sx) <= 1;
-                    push = member && qvalid;
-                    cpos = t_pos[row];
-                }
-                const unsigned long long pm = __ballot(push);
-                if (pm) {
-                    if (push) {
+                const bool hr = gh[g4] && hit_in(acc, r, first, width);
+                const unsigned long long m = __ballot(hr);
+                if (m) {
+                    if (hr) {
+                        const int row = 8 * g4 + 4 * h + rr;
                         const int s = q_size + (int)__builtin_amdgcn_mbcnt_hi(
-                                          (unsigned)(pm >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)pm, 0u));
+                                                  (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
                         if (s < kQueueCap) {
                             s_qn[s] = (unsigned char)n;
-                            s_qpos[s] = cpos;
+                            s_qpos[s] = t_pos[row];
                         } else {
                             ++c_ovf;
                         }
                         ++c_hit;
                     }
-                    q_size += __popcll(pm);
+                    q_size += __popcll(m);
                 }
             }
         }
@@ -626,7 +625,7 @@ void search_kernel(SearchArgs a) {
     };
 
     // Append at most one run per lane (in lane order) to the ring.
-    auto append_runs = [&](int start, int len, int x, int seg) __attribute__((always_inline)) {
+    auto append_runs = [&](int start, int len) __attribute__((always_inline)) {
         const bool has = len > 0;
         const unsigned long long mask = __ballot(has);
         if (mask == 0) return;
@@ -643,8 +642,6 @@ void search_kernel(SearchArgs a) {
             r_start[slot] = start;
             r_vbeg[slot] = v_total + incl - len;
             r_vend[slot] = v_total + incl;
-            r_x[slot] = x;
-            r_seg[slot] = seg;
         }
         ring_head += __popcll(mask);
         v_total += total;
@@ -653,8 +650,8 @@ void search_kernel(SearchArgs a) {
 
     if constexpr (BF) {
         if (qvalid && h == 0) c_shell += a.N;
-        my_seg = qvalid ? 0 : -1;
-        append_runs(0, lane == 0 ? a.N : 0, 0, 0);
+        if (qvalid) q_vend = 0x7fffffff;
+        append_runs(0, lane == 0 ? a.N : 0);
         consume(true);
     } else {
         // Grid geometry: the frame's projected axes (first-coordinate plans)
@@ -731,22 +728,26 @@ void search_kernel(SearchArgs a) {
         // loop below is inlined once.  A refined cell whose window is narrower
         // than the cell contributes one run per sub-bin row of the window, over
         // successive iterations of the same batch.
-        int seg = 0, seg_id = -1;
+        int seg = 0;
         int ib = 0, NI = 0;
         int kk = 0, kmax = 0;               // sub-run index within the batch (wave-uniform)
         int xa = 0, nx = 1, nq1 = 1, qlo0 = 0, qlo1 = 0, qhi1 = 0, nb2 = 1;
         bool windowed = false;              // the segment's window excludes some sub-bins
-        // this lane's cell of the current batch: sorted range, cell x, and the
+        // this lane's cell of the current batch: cell id, sorted range, and the
         // number of runs it contributes (0, 1, or nq1 for a windowed big cell)
-        int c_cell = 0, c_start = 0, c_end = 0, c_x = 0, c_runs = 0;
+        int c_cell = 0, c_start = 0, c_end = 0, c_runs = 0;
         float thr_seg = 0.0f;
         bool last = false;
         while (!last) {
             if (ib >= NI && seg < nq) {
-                ++seg_id;
                 const int R = __shfl(row_n, seg);
                 const bool in_seg = (row_n == R);
-                if (in_seg) my_seg = seg_id;
+                // the previous segment's stream ends here, this one's starts
+                if (q_vend == 0x7fffffff) q_vend = v_total;
+                if (in_seg) {
+                    q_vbeg = v_total;
+                    q_vend = 0x7fffffff;
+                }
                 const int xlo = wave_min_i32(in_seg ? x_n : 0x7fffffff);
                 const int xhi = wave_max_i32(in_seg ? x_n : -1);
                 // next segment: the queries past those with row <= R (rows are
@@ -840,7 +841,6 @@ void search_kernel(SearchArgs a) {
                                 lb = fmaf(gp, gp, lb);
                             }
                         }
-                        c_x = x;
                         if (ok) {
                             c_cell = x + Rb;
                             c_start = a.start[c_cell];
@@ -866,7 +866,7 @@ void search_kernel(SearchArgs a) {
                         rl = c_end - c_start;
                     }
                 }
-                append_runs(rs, rl, c_x, seg_id);
+                append_runs(rs, rl);
                 if (++kk >= kmax) {
                     kk = 0;
                     ib += kWave;
