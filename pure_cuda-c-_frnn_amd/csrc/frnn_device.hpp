@@ -61,24 +61,21 @@ __device__ __forceinline__ float key_d2(unsigned long long key) {
     return __uint_as_float((unsigned int)(key >> 32));
 }
 
-// Value of lane (lane ^ j) for j = 1, 2, 4, 8, 16, 32 without LDS traffic
-// where the hardware allows: DPP quad permutes (1, 2), a row rotation by 8
-// within 16-lane rows (8), the gfx950 row swaps (16, 32), and a swizzle (4).
+// Value of lane (lane ^ j) for j = 1, 2, 4, 8, 16, 32: DPP moves for 1, 2
+// (quad permutes) and 8 (rotation by 8 within 16-lane rows), the LDS
+// crossbar for the rest (swizzle xor 4 and xor 16 within 32-lane halves,
+// a backward permute for 32), which keeps those exchanges off the VALU.
 // j must fold to a constant (loops over it are fully unrolled).
 __device__ __forceinline__ unsigned xor_lane_u32(unsigned v, int j) {
-    const unsigned lane = threadIdx.x & (kWave - 1);
     switch (j) {
-        case 1: return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
-        case 2: return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
-        case 4: return (unsigned)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);      // bitmask mode, xor 4
-        case 8: return __builtin_amdgcn_update_dpp(0u, v, 0x128, 0xF, 0xF, false);  // row_ror:8
-        case 16: {
-            const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-            return (lane & 16) ? p[0] : p[1];
-        }
+        case 1: return (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
+        case 2: return (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+        case 4: return (unsigned)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);              // bitmask mode, xor 4
+        case 8: return (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true);  // row_ror:8
+        case 16: return (unsigned)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);             // bitmask mode, xor 16
         default: {
-            const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-            return (lane & 32) ? p[0] : p[1];
+            const int lane = (int)(threadIdx.x & (kWave - 1));
+            return (unsigned)__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, (int)v);
         }
     }
 }
