@@ -56,12 +56,11 @@ def build_bytes(N, D, ds, g, C, framed):
     }
     if framed:
         # frame: covariance sample over the T projection terms (512 tiles of 256
-        # points); refine: big-cell flags scan + sub-bin count (cell, count,
-        # big-cell index, T terms; writes rank and key) + sub-bin fill and scan;
-        # the reorder also reads the keys
-        nsub = (N // 256) * 1024 + 1
+        # points); refine: big-cell flags scan + the sub-bin pass's reads of
+        # every point's cell and count; the reorder also reads the keys
         b["frame"] = 4 * T * min(N, 512 * 256)
-        b["refine"] = 8 * (C + 1) + (20 + 4 * T) * N + 12 * nsub
+        # (the sub-bin work of big-cell points is data dependent and not counted)
+        b["refine"] = 8 * (C + 1) + 8 * N
         b["reorder"] += 4 * N
     return b
 
