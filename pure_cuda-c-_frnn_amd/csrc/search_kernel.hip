@@ -269,11 +269,18 @@ void search_kernel(SearchArgs a) {
         unsigned long long* L = lists + (size_t)qn * a.cap;
         // the list entries were stored by other lanes of this wave
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        unsigned long long b[EN];
+        // new keys and the sorted prefix in one round trip (the prefix loads
+        // stay in flight during the sort)
+        unsigned long long b[EN], av[EK];
 #pragma unroll
         for (int e = 0; e < EN; ++e) {
             const int i = m + e * kWave + lane;
             b[e] = (i < c) ? L[i] : ~0ull;
+        }
+#pragma unroll
+        for (int e = 0; e < EK; ++e) {
+            const int i = e * kWave + lane;
+            av[e] = (i < m) ? L[i] : ~0ull;
         }
         wave_sort_u64<EN>(b);
         unsigned long long x[EK];
@@ -284,10 +291,8 @@ void search_kernel(SearchArgs a) {
             unsigned long long cm[EK];
 #pragma unroll
             for (int e = 0; e < EK; ++e) {
-                const int i = e * kWave + lane;
-                const unsigned long long av = (i < m) ? L[i] : ~0ull;
                 const unsigned long long rb = shfl_u64(x[EK - 1 - e], kWave - 1 - lane);
-                cm[e] = av < rb ? av : rb;
+                cm[e] = av[e] < rb ? av[e] : rb;
             }
 #pragma unroll
             for (int e = 0; e < EK; ++e) x[e] = cm[e];
@@ -487,21 +492,31 @@ void search_kernel(SearchArgs a) {
         const int lane_code = (h << 7) | n;   // (4h << 5) | n
         int first, width;
         rows_of(t.v0, t.count, first, width);
+        // fast path: every lane takes all of its rows or none (the tile lies
+        // inside or outside each query's segment range and is full)
+        const bool whole = (first == -4 * h && width == 32) || width == 0;
+        const bool fast = __ballot(!whole) == 0;
+        const bool take = width != 0;
         int total = 0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const bool hr = hit_in(acc, r, first, width);
+        auto push = [&](int r, bool hr) __attribute__((always_inline)) {
             const unsigned long long m = __ballot(hr);
             if (m) {
                 if (hr) {
                     const int off = total + (int)__builtin_amdgcn_mbcnt_hi(
                                                 (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
                     s_hit[off] = (unsigned short)(((8 * (r >> 2) + (r & 3)) << 5) + lane_code);
-                    ++c_hit;
                 }
                 total += __popcll(m);
             }
+        };
+        if (fast) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) push(r, take && !(acc[r] >= thr_f));
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) push(r, hit_in(acc, r, first, width));
         }
+        if (lane == 0) c_hit += total;
         if (total == 0) return;
         lds_sync();
         for (int base = 0; base < total; base += kWave) {
