@@ -410,10 +410,10 @@ constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 
 // Principal directions and geometry of a frame (fp64, one wave; lane t holds
 // component t of every direction).  The m = g + L leading eigenvectors of the
-// sampled covariance C come from subspace iteration on (C / cmax)^4 (two
-// squarings in LDS, then 4 steps: 16 steps' worth on C; modified
-// Gram-Schmidt) and a final Rayleigh-Ritz step on C (cyclic Jacobi on the
-// m x m projected matrix, in registers).  Directions 0..g-1 become the grid axes, the next L the refinement
+// sampled covariance C come from orthogonal iteration on (C / cmax)^8 (three
+// squarings in LDS, then 2 steps: 16 steps' worth on C; modified
+// Gram-Schmidt); each direction's variance is its Rayleigh quotient on C.
+// Directions 0..g-1 become the grid axes, the next L the refinement
 // directions (slots 4, 5); weights are scaled by 1 - 2^-18, so the fp32 grid
 // directions stay orthonormal up to a shrink (|U d| <= |d| for any d) and
 // every direction has norm < 1.
@@ -488,6 +488,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     };
     square(s_P, s_A);
     square(s_A, s_P);
+    square(s_P, s_A);   // s_A = (C / cmax)^8
     double v[kMaxDirs];
 #pragma unroll
     for (int j = 0; j < kMaxDirs; ++j)
@@ -541,94 +542,31 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
             if (!on) w[j] = 0.0;
     };
     orthonormalise();
-    for (int it = 0; it < 4; ++it) {
+    for (int it = 0; it < 2; ++it) {
         double w[kMaxDirs];
-        matvec(s_P, w);
+        matvec(s_A, w);
 #pragma unroll
         for (int j = 0; j < kMaxDirs; ++j) v[j] = w[j];
         orthonormalise();
     }
-    // Rayleigh-Ritz: H = V^T C V (wave sums, so every lane holds all of H),
-    // eigen-decomposed by cyclic Jacobi in registers, redundantly on every
-    // lane (identical operations, identical results)
-    double H[kMaxDirs][kMaxDirs], R[kMaxDirs][kMaxDirs];
+    // Orthogonal iteration leaves direction j converged towards eigenvector j
+    // (descending eigenvalues); its variance is the Rayleigh quotient v_j' C v_j.
+    // A rotation inside the subspace would not change the captured variance,
+    // and the order only steers which directions grid and which refine.
+    double lam[kMaxDirs];
     {
         double w[kMaxDirs];
         matvec(s_C, w);
 #pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j)
-#pragma unroll
-            for (int k = 0; k < kMaxDirs; ++k) {
-                H[j][k] = (j < m && k < m) ? wave_sum_f64(v[j] * w[k]) : 0.0;
-                R[j][k] = (j == k) ? 1.0 : 0.0;
-            }
+        for (int j = 0; j < kMaxDirs; ++j) lam[j] = (j < m) ? wave_sum_f64(v[j] * w[j]) : 0.0;
     }
-#pragma unroll
-    for (int j = 0; j < kMaxDirs; ++j)
-#pragma unroll
-        for (int k = j + 1; k < kMaxDirs; ++k) {
-            const double sym = 0.5 * (H[j][k] + H[k][j]);
-            H[j][k] = sym;
-            H[k][j] = sym;
-        }
-    for (int sweep = 0; sweep < 20; ++sweep) {
-        double off = 0.0, dia = 0.0;
-#pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j) {
-            dia += H[j][j] * H[j][j];
-#pragma unroll
-            for (int k = j + 1; k < kMaxDirs; ++k) off += H[j][k] * H[j][k];
-        }
-        if (!(off > 1.0e-28 * dia) || !(off > 1.0e-300)) break;
-#pragma unroll
-        for (int pp = 0; pp < kMaxDirs; ++pp)
-#pragma unroll
-            for (int q = pp + 1; q < kMaxDirs; ++q) {
-                const double apq = H[pp][q];
-                if (q < m && fabs(apq) > 1.0e-300) {
-                    const double th = (H[q][q] - H[pp][pp]) / (2.0 * apq);
-                    const double tt = (th >= 0.0 ? 1.0 : -1.0) / (fabs(th) + sqrt(th * th + 1.0));
-                    const double cs = 1.0 / sqrt(tt * tt + 1.0), sn = tt * cs;
-#pragma unroll
-                    for (int k = 0; k < kMaxDirs; ++k) {   // columns pp, q of H
-                        const double hkp = H[k][pp], hkq = H[k][q];
-                        H[k][pp] = cs * hkp - sn * hkq;
-                        H[k][q] = sn * hkp + cs * hkq;
-                    }
-#pragma unroll
-                    for (int k = 0; k < kMaxDirs; ++k) {   // rows pp, q of H
-                        const double hpk = H[pp][k], hqk = H[q][k];
-                        H[pp][k] = cs * hpk - sn * hqk;
-                        H[q][k] = sn * hpk + cs * hqk;
-                    }
-#pragma unroll
-                    for (int k = 0; k < kMaxDirs; ++k) {   // eigenvector columns
-                        const double rkp = R[k][pp], rkq = R[k][q];
-                        R[k][pp] = cs * rkp - sn * rkq;
-                        R[k][q] = sn * rkp + cs * rkq;
-                    }
-                }
-            }
-    }
-    // eigenvalues descending (ties: lower index first): selection by rank
-    double lam[kMaxDirs];
-#pragma unroll
-    for (int j = 0; j < kMaxDirs; ++j) lam[j] = H[j][j];
     constexpr double kShrink = 1.0 - 3.814697265625e-06;   // 1 - 2^-18
 #pragma unroll
-    for (int col = 0; col < kMaxDirs; ++col) {
-        if (col >= m) break;
-        int rank = 0;
-#pragma unroll
-        for (int k = 0; k < kMaxDirs; ++k)
-            if (k < m) rank += (lam[k] > lam[col] || (lam[k] == lam[col] && k < col)) ? 1 : 0;
-        double u = 0.0;
-#pragma unroll
-        for (int k = 0; k < kMaxDirs; ++k)
-            if (k < m) u = fma(R[k][col], v[k], u);
-        const int slot = rank < g ? rank : kRefDir0 + (rank - g);
-        if (on) f->dir[slot][t] = (float)(u * kShrink);
-        if (t == 0) f->sigma[slot] = (float)sqrt(fmax(lam[col], 0.0));
+    for (int j = 0; j < kMaxDirs; ++j) {
+        if (j >= m) break;
+        const int slot = j < g ? j : kRefDir0 + (j - g);
+        if (on) f->dir[slot][t] = (float)(v[j] * kShrink);
+        if (t == 0) f->sigma[slot] = (float)sqrt(fmax(lam[j], 0.0));
     }
     if (t != 0) return;
     // ---- geometry (one thread) ----
