@@ -62,6 +62,44 @@ __device__ __forceinline__ void lds_sync() {
 constexpr int kRing = 128;                   // pending candidate runs (<= 31 + 64 in use)
 constexpr int kMaxG = 9;
 
+// Traversal order of a segment's 3^m neighbouring rows (m = g - 1 axes): by
+// the number of axes on which the row is offset (the segment's own row, then
+// faces, edges, corners), so the nearest candidates stream first and a list's
+// first compaction already sets a threshold near its K-th distance.  Entries
+// are natural row indices, digit d (0, 1, 2) = offset -1, 0, +1 on axis d + 1.
+struct RowOrder { unsigned char v[27]; };
+constexpr RowOrder make_row_order(int m) {
+    RowOrder r{};
+    int n = 1;
+    for (int i = 0; i < m; ++i) n *= 3;
+    int k = 0;
+    for (int w = 0; w <= m; ++w)
+        for (int t = 0; t < n; ++t) {
+            int tt = t, nz = 0;
+            for (int d = 0; d < m; ++d) {
+                nz += (tt % 3) != 1;
+                tt /= 3;
+            }
+            if (nz == w) r.v[k++] = (unsigned char)t;
+        }
+    return r;
+}
+__constant__ RowOrder kRowOrder[4] = {make_row_order(0), make_row_order(1), make_row_order(2),
+                                      make_row_order(3)};
+// natural index of the o-th row in traversal order; more than 3 row axes map
+// each base-3 digit 0, 1, 2 to offset 0, -1, +1 (own row first)
+__device__ __forceinline__ int natural_row(int o, int m) {
+    if (m <= 3) return kRowOrder[m].v[o];
+    int t = 0, p = 1;
+    for (int d = 0; d < m; ++d) {
+        const int dg = o % 3;
+        o /= 3;
+        t += (dg == 0 ? 1 : dg == 1 ? 0 : 2) * p;
+        p *= 3;
+    }
+    return t;
+}
+
 struct SearchArgs {
     const float* pts;            // AoS rows, stride DS (sorted order for grids)
     const float* frows;          // the same rows centred, fl(x - mean) (wide rows only)
@@ -752,11 +790,13 @@ void search_kernel(SearchArgs a) {
         // number of runs it contributes (0, 1, or nq1 for a windowed big cell)
         int c_cell = 0, c_start = 0, c_end = 0, c_runs = 0;
         float thr_seg = 0.0f;
+        bool seg_mine = false;              // this lane's query is in the current segment
         bool last = false;
         while (!last) {
             if (ib >= NI && seg < nq) {
                 const int R = __shfl(row_n, seg);
                 const bool in_seg = (row_n == R);
+                seg_mine = in_seg;
                 // the previous segment's stream ends here, this one's starts
                 if (q_vend == 0x7fffffff) q_vend = v_total;
                 if (in_seg) {
@@ -780,7 +820,6 @@ void search_kernel(SearchArgs a) {
                         s_rc[d] = d > 0 ? (R / s_stride[d]) % s_res[d] : 0;
                     }
                 }
-                thr_seg = wave_max_f32(in_seg ? key_d2(s_thr[n]) : -__builtin_huge_valf());
                 // refinement windows: a candidate within the radius of a segment
                 // query q has |s(p) - s(q)| <= |p - q| + 2 margin on each direction
                 // (weights of norm < 1), so its projection lies in [lo - h, hi + h]
@@ -833,12 +872,16 @@ void search_kernel(SearchArgs a) {
             }
             if (ib < NI) {
                 if (kk == 0) {
+                    // the segment's largest threshold, as tightened by the
+                    // compactions so far (cells beyond it hold no candidate
+                    // any of its queries would still accept)
+                    thr_seg = wave_max_f32(seg_mine ? key_d2(s_thr[n]) : -__builtin_huge_valf());
                     // this lane's cell: AABB test against the segment's queries
                     const int item = ib + lane;
                     c_runs = 0;
                     if (item < NI) {
                         const int x = xa + item % nx;
-                        int tt = item / nx, Rb = 0;
+                        int tt = natural_row(item / nx, G - 1), Rb = 0;
                         bool ok = true;
                         float lb = 0.0f;
                         {
