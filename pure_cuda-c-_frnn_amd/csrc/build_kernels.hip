@@ -400,8 +400,9 @@ __global__ __launch_bounds__(256) void cov_reduce_kernel(const double* __restric
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
     for (int lj = 0; lj < 6; ++lj) {
-        const unsigned long long u = xor_lane_u64((unsigned long long)__double_as_longlong(v), 1 << lj);
-        v += __longlong_as_double((long long)u);
+        unsigned long long a, b;
+        xor_pair_u64((unsigned long long)__double_as_longlong(v), 1 << lj, a, b);
+        v = __longlong_as_double((long long)a) + __longlong_as_double((long long)b);
     }
     return v;
 }

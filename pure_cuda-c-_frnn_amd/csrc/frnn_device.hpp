@@ -61,29 +61,52 @@ __device__ __forceinline__ float key_d2(unsigned long long key) {
     return __uint_as_float((unsigned int)(key >> 32));
 }
 
-// Value of lane (lane ^ j) for j = 1, 2, 4, 8, 16, 32: DPP moves for 1, 2
-// (quad permutes) and 8 (rotation by 8 within 16-lane rows), the LDS
-// crossbar for the rest (swizzle xor 4 and xor 16 within 32-lane halves,
-// a backward permute for 32), which keeps those exchanges off the VALU.
+// Lane exchanges at xor distance j = 1, 2, 4, 8, 16, 32, all on the VALU
+// (no LDS round trip, which would put its latency on every step of a
+// dependent sort or reduction).  xor_pair_u32 yields {v(lane), v(lane ^ j)}
+// as (a, b) in a lane-dependent order, which is all a symmetric
+// compare-exchange, min, max or sum needs:
+//   j = 1, 2  DPP quad permutes [1,0,3,2] / [2,3,0,1]
+//   j = 4     DPP row rotations by 4 and 12 (lanes with bit 2 set take the
+//             one reading lane - 4)
+//   j = 8     DPP row_ror:8
+//   j = 16    v_permlane16_swap (rows 0/1 and 2/3 of a and b hold each other)
+//   j = 32    v_permlane32_swap (the two 32-lane halves)
 // j must fold to a constant (loops over it are fully unrolled).
-__device__ __forceinline__ unsigned xor_lane_u32(unsigned v, int j) {
+__device__ __forceinline__ void xor_pair_u32(unsigned v, int j, unsigned& a, unsigned& b) {
     switch (j) {
-        case 1: return (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
-        case 2: return (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
-        case 4: return (unsigned)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);              // bitmask mode, xor 4
-        case 8: return (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true);  // row_ror:8
-        case 16: return (unsigned)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);             // bitmask mode, xor 16
+        case 1: a = v; b = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true); return;
+        case 2: a = v; b = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true); return;
+        case 4: {
+            const unsigned dn = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true);  // lane - 4
+            const unsigned up = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x12C, 0xF, 0xF, true);  // lane + 4
+            a = v;
+            b = (threadIdx.x & 4) ? dn : up;
+            return;
+        }
+        case 8: a = v; b = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true); return;
+        case 16: {
+            const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+            a = r[0];
+            b = r[1];
+            return;
+        }
         default: {
-            const int lane = (int)(threadIdx.x & (kWave - 1));
-            return (unsigned)__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, (int)v);
+            const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+            a = r[0];
+            b = r[1];
+            return;
         }
     }
 }
 
-__device__ __forceinline__ unsigned long long xor_lane_u64(unsigned long long v, int j) {
-    const unsigned lo = xor_lane_u32((unsigned)v, j);
-    const unsigned hi = xor_lane_u32((unsigned)(v >> 32), j);
-    return ((unsigned long long)hi << 32) | lo;
+__device__ __forceinline__ void xor_pair_u64(unsigned long long v, int j, unsigned long long& a,
+                                             unsigned long long& b) {
+    unsigned alo, blo, ahi, bhi;
+    xor_pair_u32((unsigned)v, j, alo, blo);
+    xor_pair_u32((unsigned)(v >> 32), j, ahi, bhi);
+    a = ((unsigned long long)ahi << 32) | alo;
+    b = ((unsigned long long)bhi << 32) | blo;
 }
 
 __device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int src) {
@@ -113,11 +136,11 @@ __device__ __forceinline__ void bitonic_step(unsigned long long (&x)[E], int k, 
     } else {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const unsigned long long y = xor_lane_u64(x[e], j);
+            unsigned long long p, q;
+            xor_pair_u64(x[e], j, p, q);
             const bool up = (((e * kWave) | lane) & k) == 0;
             const bool keep_min = ((lane & j) == 0) == up;
-            const bool lt = x[e] < y;
-            x[e] = (lt == keep_min) ? x[e] : y;
+            x[e] = ((p < q) == keep_min) ? p : q;
         }
     }
 }
@@ -144,29 +167,50 @@ __device__ __forceinline__ void wave_bitonic_merge_u64(unsigned long long (&x)[E
     for (int lj = log2_keys<E>() - 1; lj >= 0; --lj) bitonic_step<E>(x, 0, 1 << lj);
 }
 
+// Wave-wide reductions over the VALU lane exchanges above.
 __device__ __forceinline__ int wave_min_i32(int v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned p, q;
+        xor_pair_u32((unsigned)v, o, p, q);
+        v = min((int)p, (int)q);
+    }
     return v;
 }
 __device__ __forceinline__ int wave_max_i32(int v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned p, q;
+        xor_pair_u32((unsigned)v, o, p, q);
+        v = max((int)p, (int)q);
+    }
     return v;
 }
 __device__ __forceinline__ float wave_min_f32(float v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned p, q;
+        xor_pair_u32(__float_as_uint(v), o, p, q);
+        v = fminf(__uint_as_float(p), __uint_as_float(q));
+    }
     return v;
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned p, q;
+        xor_pair_u32(__float_as_uint(v), o, p, q);
+        v = fmaxf(__uint_as_float(p), __uint_as_float(q));
+    }
     return v;
 }
 __device__ __forceinline__ long long wave_sum_i64(long long v) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned long long p, q;
+        xor_pair_u64((unsigned long long)v, o, p, q);
+        v = (long long)(p + q);
+    }
     return v;
 }
 

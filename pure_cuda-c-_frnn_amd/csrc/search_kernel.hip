@@ -276,7 +276,9 @@ void search_kernel(SearchArgs a) {
             pn = fmaf(c0, c0, pn);
             pn = fmaf(c1, c1, pn);
         }
-        qn2 = pn + __shfl_xor(pn, 32);
+        unsigned pa, pb;
+        xor_pair_u32(__float_as_uint(pn), 32, pa, pb);
+        qn2 = __uint_as_float(pa) + __uint_as_float(pb);
         bop[HD] = (h == 0) ? a.norm_scale : qn2 * a.norm_scale;
     }
     if (!qvalid) {
@@ -472,7 +474,9 @@ void search_kernel(SearchArgs a) {
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(c, bop[j], acc, 0, 0, 0);
             pn = fmaf(c, c, pn);
         }
-        const float nrm = pn + __shfl_xor(pn, 32);
+        unsigned pa, pb;
+        xor_pair_u32(__float_as_uint(pn), 32, pa, pb);
+        const float nrm = __uint_as_float(pa) + __uint_as_float(pb);
         cand_norm = nrm;
         const float last = (h == 0) ? (n < t.count ? nrm : 3.0e38f) : 1.0f;
         return __builtin_amdgcn_mfma_f32_32x32x2f32(last, bop[HD], acc, 0, 0, 0);
