@@ -160,19 +160,25 @@ int frnn_engine_set_stream(frnn_engine_t* engine, void* hip_stream);
 /* Plan used by the last search. */
 int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
 
-/* Per-stage HIP event timing (replaces the reference's FRNN_REPORT_OCCUPANCY
- * diagnostics, find_nbrs.cu:355-382).  Stages: 0 zero-fill, 1 point
- * statistics, 2 grid frame, 3 bin+count, 4 scan, 5 within-cell refinement,
- * 6 reorder/transpose, 7 neighbour search, 8 unpermute. */
+/* Profiling (replaces the reference's FRNN_REPORT_OCCUPANCY diagnostics,
+ * find_nbrs.cu:355-382).  flags: FRNN_PROFILE_EVENTS records per-stage HIP
+ * events; FRNN_PROFILE_COUNTERS runs the counting build of the search kernel
+ * and reads its work counters back after each search (0: neither).  Stages:
+ * 0 zero-fill, 1 point statistics, 2 grid frame, 3 bin+count, 4 scan,
+ * 5 within-cell refinement, 6 reorder/transpose, 7 neighbour search,
+ * 8 unpermute. */
 #define FRNN_NUM_STAGES 9
-int frnn_engine_set_profiling(frnn_engine_t* engine, int enable);
+#define FRNN_PROFILE_EVENTS 1
+#define FRNN_PROFILE_COUNTERS 2
+int frnn_engine_set_profiling(frnn_engine_t* engine, int flags);
 int frnn_engine_stage_times(const frnn_engine_t* engine, float* ms, int n);
-/* Work counters of the last profiled search: [0] shell candidates (sum over
- * queries of the points in their 3^g cells, or N per query for brute force),
- * [1] pairs passing the MFMA filter, [2] pairs accepted after the exact check,
- * [3] query-candidate pairs streamed through the MFMA filter (after the
- * window and AABB pruning).  A profiled search also fails with FRNN_ERR_HIP
- * if the kernel's internal capacity guards ever fired. */
+/* Work counters of the last search run with FRNN_PROFILE_COUNTERS:
+ * [0] shell candidates (sum over queries of the points in their 3^g cells,
+ * or N per query for brute force), [1] pairs passing the MFMA filter,
+ * [2] pairs accepted after the exact check, [3] query-candidate pairs
+ * streamed through the MFMA filter (after the window and AABB pruning).
+ * Such a search also fails with FRNN_ERR_HIP if the kernel's internal
+ * capacity guards ever fired. */
 #define FRNN_NUM_COUNTERS 4
 int frnn_engine_counters(const frnn_engine_t* engine, long long* out, int n);
 

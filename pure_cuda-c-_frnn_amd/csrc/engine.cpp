@@ -112,7 +112,8 @@ struct frnn_engine {
     frnn_plan_t last_plan{};
     bool has_result = false;
     int last_N = 0, last_K = 0;
-    bool profiling = false;
+    bool profiling = false;   // per-stage HIP events
+    bool counting = false;    // work counters (the counting search kernel)
     hipEvent_t ev[FRNN_NUM_STAGES + 1] = {};
     float stage_ms[FRNN_NUM_STAGES] = {};
     long long ctr[FRNN_NUM_COUNTERS] = {};
@@ -163,11 +164,10 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
                     "allocating the grid frame"));
         frame = e->frame_ws;
     }
-    if (e->profiling) {
+    if (e->counting)
         ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * kCounterSlots, 0, s),
                              "clearing counters"));
-        HIP_TRY(hipEventRecord(e->ev[0], s), "event record");
-    }
+    if (e->profiling) HIP_TRY(hipEventRecord(e->ev[0], s), "event record");
     auto mark = [&](int i) -> int {
         if (e->profiling) HIP_TRY(hipEventRecord(e->ev[i], s), "event record");
         return FRNN_OK;
@@ -215,7 +215,7 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     ST_TRY(launch_status(frnn::launch_search(e->aos, frows, e->stats_ws, grid ? e->sorted_idx : nullptr,
                                              grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
                                              N, dim, K, plan, e->lists, cap,
-                                             e->profiling ? e->counters : nullptr, s),
+                                             e->counting ? e->counters : nullptr, s),
                          "search launch"));
     ST_TRY(mark(8));
     // stage 8: results to the original query order (ScatterToOrigKernel)
@@ -224,9 +224,10 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
                          "unpermute launch"));
     ST_TRY(mark(9));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
-    if (e->profiling) {
+    if (e->profiling)
         for (int i = 0; i < FRNN_NUM_STAGES; ++i)
             HIP_TRY(hipEventElapsedTime(&e->stage_ms[i], e->ev[i], e->ev[i + 1]), "event timing");
+    if (e->counting) {
         unsigned long long c[kCounterSlots];
         HIP_TRY(hipMemcpy(c, e->counters, sizeof(c), hipMemcpyDeviceToHost), "reading counters");
         for (int i = 0; i < FRNN_NUM_COUNTERS; ++i) e->ctr[i] = (long long)c[i];
@@ -451,9 +452,12 @@ int frnn_engine_last_plan(const frnn_engine_t* e, frnn_plan_t* out) {
     return FRNN_OK;
 }
 
-int frnn_engine_set_profiling(frnn_engine_t* e, int enable) {
+int frnn_engine_set_profiling(frnn_engine_t* e, int flags) {
     if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
-    e->profiling = enable != 0;
+    if (flags & ~(FRNN_PROFILE_EVENTS | FRNN_PROFILE_COUNTERS))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "unknown profiling flags");
+    e->profiling = (flags & FRNN_PROFILE_EVENTS) != 0;
+    e->counting = (flags & FRNN_PROFILE_COUNTERS) != 0;
     return FRNN_OK;
 }
 

@@ -161,13 +161,18 @@ __device__ __forceinline__ float exact_d2(const float* q, const float* __restric
     return acc;
 }
 
-// Small padded dimensions keep three waves per SIMD resident (register budget
-// 168), larger ones two (256 VGPRs + AGPRs), so a second wave's MFMA chain can
-// overlap one wave's hit handling.
+// Rows of up to 16 floats keep four waves per SIMD resident (register budget
+// 128; the search is bound by the latency of its gathers, list round trips
+// and sorts, so the extra wave outweighs a few spilled registers), larger ones
+// two (256 VGPRs + AGPRs), so a second wave's MFMA chain can overlap one
+// wave's hit handling.
 template <int DS>
-struct WavesPerEU { static constexpr int value = DS <= 16 ? 3 : 2; };
+struct WavesPerEU { static constexpr int value = DS <= 16 ? 4 : 2; };
 
-template <int DS, bool REV, bool BF>
+// CNT: the profiling build of the kernel, which also keeps the work counters
+// (a separate instantiation, so the counting code costs the plain kernel no
+// registers).
+template <int DS, bool REV, bool BF, bool CNT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DS>::value)))
 void search_kernel(SearchArgs a) {
     constexpr int HD = DS / 2;
@@ -183,6 +188,7 @@ void search_kernel(SearchArgs a) {
     __shared__ int s_cnt[kQB];
     __shared__ int s_srt[kQB];       // sorted prefix length of each list
     __shared__ unsigned long long s_thr[kQB];
+    __shared__ unsigned long long s_ctr[5];
     // Rows of up to 32 floats re-evaluate a tile's hits right after its MFMA
     // chain, from the tile's raw rows staged in LDS; wider rows queue hits as
     // (query, sorted position) and re-evaluate them 64 at a time from memory.
@@ -234,6 +240,7 @@ void search_kernel(SearchArgs a) {
     }
     // row of query qn (a valid query of the chunk; queue path, wide rows)
     auto query_row = [&](int qn) -> const float* { return a.pts + (size_t)(q0 + qn) * DS; };
+    if (CNT && lane < 5) s_ctr[lane] = 0;
     if (lane < kQB) {
         s_cnt[lane] = 0;
         s_srt[lane] = 0;
@@ -290,7 +297,13 @@ void search_kernel(SearchArgs a) {
     // per-value (NaN-aware) hit test.
     const bool robust_q = __ballot(qvalid && !(qn2 < 1.0e37f)) != 0;
 
-    long long c_shell = 0, c_hit = 0, c_acc = 0, c_ovf = 0, c_stream = 0;
+    // Profiling counters (CNT): wave totals kept in LDS by lane 0 from ballot
+    // counts.  Slots: shell candidates, filter hits, accepted keys, streamed
+    // (query, candidate) pairs, list/queue capacity overflows.
+    constexpr bool counting = CNT;
+    auto bump = [&](int i, unsigned long long v) __attribute__((always_inline)) {
+        if (counting && lane == 0) s_ctr[i] += v;
+    };
     int q_size = 0;                     // queue entries (wave-uniform)
 
     // Selection on query qn's candidate list.  A list keeps its first s_srt[qn]
@@ -397,20 +410,25 @@ void search_kernel(SearchArgs a) {
             }
             if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
         }
+        bool accepted = false, ovf = false;
         if (!kTileExact && lane < count) {
             const int qn = s_qn[base + lane];
             const int pos = s_qpos[base + lane];
             const float e = exact_d2<DS, REV>(query_row(qn), a.pts + (size_t)pos * DS);
             const int idx = BF ? pos : a.sorted_idx[pos];
             const unsigned long long key = make_key(e, idx);
-            if (key < s_thr[qn]) {
+            accepted = key < s_thr[qn];
+            if (accepted) {
                 const int slot = atomicAdd(&s_cnt[qn], 1);
                 // compaction above leaves >= kBatch free slots; the guard only
                 // keeps a logic error from writing past the list
                 if (slot < a.room) lists[(size_t)qn * a.cap + slot] = key;
-                else ++c_ovf;
-                ++c_acc;
+                else ovf = true;
             }
+        }
+        if constexpr (counting) {
+            bump(2, __popcll(__ballot(accepted)));
+            bump(4, __popcll(__ballot(ovf)));
         }
         lds_sync();
         q_size = base;
@@ -558,7 +576,7 @@ void search_kernel(SearchArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) push(r, hit_in(acc, r, first, width));
         }
-        if (lane == 0) c_hit += total;
+        bump(1, total);
         if (total == 0) return;
         lds_sync();
         for (int base = 0; base < total; base += kWave) {
@@ -572,20 +590,25 @@ void search_kernel(SearchArgs a) {
                 }
                 if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
             }
+            bool accepted = false, ovf = false;
             if (base + lane < total) {
                 const int e = s_hit[base + lane];
                 const int qn = e & 31;
                 const int row = e >> 5;
                 const float d2 = exact_d2<DS, REV>(s_q + qn * RS, t_rows + row * RS);
                 const unsigned long long key = make_key(d2, t_idx[row]);
-                if (key < s_thr[qn]) {
+                accepted = key < s_thr[qn];
+                if (accepted) {
                     const int slot = atomicAdd(&s_cnt[qn], 1);
                     // compaction above leaves >= kBatch free slots; the guard
                     // only keeps a logic error from writing past the list
                     if (slot < a.room) lists[(size_t)qn * a.cap + slot] = key;
-                    else ++c_ovf;
-                    ++c_acc;
+                    else ovf = true;
                 }
+            }
+            if constexpr (counting) {
+                bump(2, __popcll(__ballot(accepted)));
+                bump(4, __popcll(__ballot(ovf)));
             }
             lds_sync();
         }
@@ -632,11 +655,12 @@ void search_kernel(SearchArgs a) {
                         if (s < kQueueCap) {
                             s_qn[s] = (unsigned char)n;
                             s_qpos[s] = t_pos[row];
-                        } else {
-                            ++c_ovf;
                         }
-                        ++c_hit;
                     }
+                    bump(1, __popcll(m));
+                    // entries past the queue's capacity (a logic error) are counted
+                    const int over = q_size + __popcll(m) - kQueueCap;
+                    if (over > 0) bump(4, min(over, __popcll(m)));
                     q_size += __popcll(m);
                 }
             }
@@ -669,7 +693,7 @@ void search_kernel(SearchArgs a) {
             }
             if constexpr (kTileExact) hits_tile_exact(cur, acc, cand_norm);
             else hits_queue(cur, acc, cand_norm);
-            if (h == 0 && n == 0) c_stream += cur.count;
+            bump(3, (unsigned long long)cur.count * kQB);
             v_done = vn;
             while (ring_tail < ring_head && r_vend[ring_tail & (kRing - 1)] <= v_done) ++ring_tail;
             if (!has_next) break;
@@ -706,7 +730,7 @@ void search_kernel(SearchArgs a) {
     };
 
     if constexpr (BF) {
-        if (qvalid && h == 0) c_shell += a.N;
+        bump(0, (unsigned long long)nq * a.N);
         if (qvalid) q_vend = 0x7fffffff;
         append_runs(0, lane == 0 ? a.N : 0);
         consume(true);
@@ -851,19 +875,24 @@ void search_kernel(SearchArgs a) {
                 }
                 lds_sync();
 
-                if (a.counters && in_seg && h == 0) {
-                    for (int t = 0; t < nrows; ++t) {
-                        int tt = t, Rb = 0;
-                        bool ok = true;
-                        for (int d = 1; d < G; ++d) {
-                            const int cc = s_rc[d] + (tt % 3) - 1;
-                            tt /= 3;
-                            ok = ok && cc >= 0 && cc < s_res[d];
-                            Rb += cc * s_stride[d];
+                if constexpr (counting) {
+                    // the reference's shell candidates of this segment's queries
+                    long long sh = 0;
+                    if (in_seg && h == 0) {
+                        for (int t = 0; t < nrows; ++t) {
+                            int tt = t, Rb = 0;
+                            bool ok = true;
+                            for (int d = 1; d < G; ++d) {
+                                const int cc = s_rc[d] + (tt % 3) - 1;
+                                tt /= 3;
+                                ok = ok && cc >= 0 && cc < s_res[d];
+                                Rb += cc * s_stride[d];
+                            }
+                            if (!ok) continue;
+                            sh += a.start[Rb + min(x_n + 1, res0 - 1) + 1] - a.start[Rb + max(x_n - 1, 0)];
                         }
-                        if (!ok) continue;
-                        c_shell += a.start[Rb + min(x_n + 1, res0 - 1) + 1] - a.start[Rb + max(x_n - 1, 0)];
                     }
+                    bump(0, (unsigned long long)wave_sum_i64(sh));
                 }
 
                 xa = max(xlo - 1, 0);
@@ -948,25 +977,18 @@ void search_kernel(SearchArgs a) {
         for (int pass = 0; pass < 2; ++pass) process_batch(0, pass == 0 ? qs : 0, pass == 1);
     }
 
-    if (a.counters) {
-        const long long s0 = wave_sum_i64(c_shell);
-        const long long s1 = wave_sum_i64(c_hit);
-        const long long s2 = wave_sum_i64(c_acc);
-        const long long s3 = wave_sum_i64(c_stream) * kQB;
-        const long long s4 = wave_sum_i64(c_ovf);
-        if (lane == 0) {
-            atomicAdd(&a.counters[0], (unsigned long long)s0);
-            atomicAdd(&a.counters[1], (unsigned long long)s1);
-            atomicAdd(&a.counters[2], (unsigned long long)s2);
-            atomicAdd(&a.counters[3], (unsigned long long)s3);
-            if (s4) atomicAdd(&a.counters[4], (unsigned long long)s4);
-        }
+    if constexpr (counting) {
+        lds_sync();
+        if (lane < 5 && (lane != 4 || s_ctr[4] != 0)) atomicAdd(&a.counters[lane], s_ctr[lane]);
     }
 }
 
 template <int DS, bool REV, bool BF>
 static void launch_one(const SearchArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((search_kernel<DS, REV, BF>), dim3(a.nchunks), dim3(kWave), 0, s, a);
+    if (a.counters)
+        hipLaunchKernelGGL((search_kernel<DS, REV, BF, true>), dim3(a.nchunks), dim3(kWave), 0, s, a);
+    else
+        hipLaunchKernelGGL((search_kernel<DS, REV, BF, false>), dim3(a.nchunks), dim3(kWave), 0, s, a);
 }
 
 template <int DS>

@@ -26,6 +26,7 @@ MAX_DIM = 128
 MAX_CELLS = 1_000_000
 NUM_STAGES = 9
 NUM_COUNTERS = 4
+PROFILE_EVENTS, PROFILE_COUNTERS = 1, 2
 STAGE_NAMES = ("zero_fill", "stats", "frame", "bin_count", "scan", "refine", "reorder", "search",
                "unpermute")
 PATH_NAMES = {-1: "empty", 0: "bruteforce", 1: "grid_full", 2: "grid_first"}
@@ -253,8 +254,11 @@ class FRNNEngine:
         _check(_load().frnn_engine_last_plan(self._handle(), ctypes.byref(p)), "last_plan")
         return p.as_dict()
 
-    def set_profiling(self, enable=True):
-        _check(_load().frnn_engine_set_profiling(self._handle(), int(bool(enable))), "set_profiling")
+    def set_profiling(self, enable=True, counters=True):
+        """enable: per-stage HIP event times (stage_times()); counters: also run
+        the counting build of the search kernel (counters())."""
+        flags = (PROFILE_EVENTS | (PROFILE_COUNTERS if counters else 0)) if enable else 0
+        _check(_load().frnn_engine_set_profiling(self._handle(), flags), "set_profiling")
 
     def stage_times(self):
         """Per-stage milliseconds of the last profiled search (HIP events)."""
