@@ -198,12 +198,15 @@ void search_kernel(SearchArgs a) {
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points
     // at virtual stream positions [vbeg, vend)
     __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing];
-    // current tile, per candidate row: the original index (tile-exact path)
-    // or sorted position (queue path); tile-exact path: the raw rows (stride
-    // RS, as s_q) and the hit entries (row << 5 | query)
-    __shared__ int t_idx[32];
-    __shared__ int t_pos[kTileExact ? 1 : 32];
-    __shared__ __align__(16) float t_rows[kTileExact ? 32 * RS : 4];
+    // current tile, per candidate row: the sorted position and (tile-exact
+    // path) the original index and the raw row (stride RS, as s_q), and the
+    // hit entries (row << 5 | query).  At DS = 16 (four waves per SIMD) the
+    // rows are not staged, which keeps the workgroup within a quarter of the
+    // LDS per SIMD: the exact rounds read the just-gathered rows from cache.
+    constexpr bool kStageRows = kTileExact && DS != 16;
+    __shared__ int t_pos[32];
+    __shared__ int t_idx[kTileExact ? 32 : 1];
+    __shared__ __align__(16) float t_rows[kStageRows ? 32 * RS : 4];
     __shared__ unsigned short s_hit[kTileExact ? 32 * 32 : 2];
     // grid geometry per axis (cells, cell-id stride, origin), the segment's
     // bounding box and row coordinates, and each query's grid coordinates
@@ -211,7 +214,10 @@ void search_kernel(SearchArgs a) {
     __shared__ float s_org[kMaxG];
     __shared__ float s_blo[kMaxG], s_bhi[kMaxG];
     __shared__ int s_rc[kMaxG];
-    __shared__ float s_qg[BF ? 1 : kQB * kMaxG];
+    // rows of 16 or more floats only occur on first-coordinate grids (g <= 4;
+    // a full-D grid needs res^D <= 1M cells with res > 3, so D <= 9)
+    constexpr int kGA = DS >= 16 ? kFrameGrid : kMaxG;
+    __shared__ float s_qg[BF ? 1 : kQB * kGA];
 
     const int lane = threadIdx.x;
     const int n = lane & 31;
@@ -535,7 +541,8 @@ void search_kernel(SearchArgs a) {
         return __ballot(qvalid && mn < thr_f) != 0;
     };
 
-    // Tile-exact path: the tile's raw rows and original indices go to LDS,
+    // Tile-exact path: the tile's sorted positions, original indices and
+    // (kStageRows) raw rows go to LDS,
     // the hits (row << 5 | query) are written register by register at ballot
     // prefix offsets, and they are re-evaluated in rounds of 64 lanes, each
     // round preceded by the compaction of any list that could overflow in it.
@@ -543,11 +550,14 @@ void search_kernel(SearchArgs a) {
         const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
         if (!any_hit(acc, robust)) return;
         lds_sync();
-        {
+        if (h == 0) {
+            t_pos[n] = t.pos;
+            t_idx[n] = t.idx;
+        }
+        if constexpr (kStageRows) {
             float* dst = t_rows + n * RS + h * HD;
 #pragma unroll
             for (int j = 0; j < HD; ++j) dst[j] = t.op[j];
-            if (h == 0) t_idx[n] = t.idx;
         }
         const int lane_code = (h << 7) | n;   // (4h << 5) | n
         int first, width;
@@ -595,7 +605,8 @@ void search_kernel(SearchArgs a) {
                 const int e = s_hit[base + lane];
                 const int qn = e & 31;
                 const int row = e >> 5;
-                const float d2 = exact_d2<DS, REV>(s_q + qn * RS, t_rows + row * RS);
+                const float* prow = kStageRows ? t_rows + row * RS : a.pts + (size_t)t_pos[row] * DS;
+                const float d2 = exact_d2<DS, REV>(s_q + qn * RS, prow);
                 const unsigned long long key = make_key(d2, t_idx[row]);
                 accepted = key < s_thr[qn];
                 if (accepted) {
@@ -765,12 +776,12 @@ void search_kernel(SearchArgs a) {
             if (h == 0) {
 #pragma unroll
                 for (int d = 0; d < kFrameGrid; ++d)
-                    if (d < G) s_qg[n * kMaxG + d] = sp[d];
+                    if (d < G) s_qg[n * kGA + d] = sp[d];
             }
             pj0 = sp[kRefDir0];
             pj1 = sp[kRefDir0 + 1];
         } else if (h == 0) {
-            for (int d = 0; d < G; ++d) s_qg[n * kMaxG + d] = qrow[d];
+            for (int d = 0; d < G; ++d) s_qg[n * kGA + d] = qrow[d];
         }
         // the query's cell, as binned: x along axis 0, the row as the id of
         // the row's x = 0 cell (rows are non-decreasing in the sorted order)
@@ -839,7 +850,7 @@ void search_kernel(SearchArgs a) {
                 seg = max(seg + 1, (int)__popcll(__ballot(row_n <= R) & 0xffffffffull));
                 // segment bounding box on the grid axes and the largest threshold
                 for (int d = 0; d < G; ++d) {
-                    const float qd = s_qg[n * kMaxG + d];
+                    const float qd = s_qg[n * kGA + d];
                     const float lo = wave_min_f32(in_seg ? qd : __builtin_huge_valf());
                     const float hi = wave_max_f32(in_seg ? qd : -__builtin_huge_valf());
                     if (lane == 0) {
@@ -1005,6 +1016,7 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     const bool bf = plan.path == FRNN_PATH_BRUTEFORCE;
     if (!bf && (plan.grid_dim < 1 || plan.grid_dim > kMaxG || !sorted_idx || !cell_of || !start)) return 1;
     if (!bf && frame_ws && plan.grid_dim > kFrameGrid) return 1;
+    if (!bf && aos_stride(D) >= 16 && plan.grid_dim > kFrameGrid) return 1;   // kernels size s_qg for g <= 4
     if (cap < list_capacity(K) || K > FRNN_MAX_K || !stats_ws || D < 1 || D > FRNN_MAX_DIM) return 1;
     if (uses_filter_rows(D) && !frows) return 1;
     SearchArgs a{};
