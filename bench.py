@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """All-points FRNN (grid build + neighbour search) on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config metric|C1..C5] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config metric|C1..C5|refD<D>N<N>] [--no-cpu]
 
 A step is one FRNNEngine.search_gpu call (reference: frnn_engine.cu:195-250)
 over the configuration's synthetic cloud, with the SoA input already resident
@@ -18,6 +18,8 @@ in HBM and the outputs left in HBM -- the timing the reference's harness uses
                    8DN + 4(C+1) + 4N + 8KN (read rows, cell offsets, index map;
                    write K keys per query) over the same duration vs 8 TB/s.
   build_hbm        grid-build kernels: algorithmic bytes / event time vs 8 TB/s
+  refD<D>N<N>      a cell of the reference's own published K=16 sweep (A100
+                   latency reported beside ours; frnn_workloads.REF_SWEEP)
   cpu_baseline     the C++/OpenMP restatement (oracle/) on a bounded query sample,
                    timed on this host, extrapolated to all N queries; the same
                    sample is also compared bit-exactly with the GPU rows
@@ -233,7 +235,10 @@ def main():
         "config": {"workload": w.name, "N": w.N, "D": w.D, "K": w.K, "radius": w.radius,
                    "raw_radius": w.notes.get("raw_radius"), "path": plan["path"],
                    "grid_dim": plan["grid_dim"], "res": plan["res"], "cells": plan["cells"],
-                   "queries_per_s": round(w.N / (ms_per_step / 1e3), 1)},
+                   "queries_per_s": round(w.N / (ms_per_step / 1e3), 1),
+                   **({"reference_a100_ms": round(w.notes["a100_ms"], 4),
+                       "speedup_vs_reference_a100": round(w.notes["a100_ms"] / ms_per_step, 2)}
+                      if "a100_ms" in w.notes else {})},
         "roofline": roofline,
         "build_hbm": build,
         "end_to_end_hbm": {"bytes": end_to_end_bytes, "GBps": round(e2e_gbs, 1),
