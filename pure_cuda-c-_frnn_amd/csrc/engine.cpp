@@ -133,9 +133,12 @@ void release(frnn_engine* e) {
 
 // The whole device pipeline of search_gpu on an SoA device input.
 int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius) {
-    frnn_plan_t plan;
-    ST_TRY(frnn_make_plan(N, dim, K, radius, &plan));
-    e->last_plan = plan;
+    frnn_plan_t ref_plan;
+    ST_TRY(frnn_make_plan(N, dim, K, radius, &ref_plan));
+    e->last_plan = ref_plan;
+    // the grid the kernels bin and search on (the reference's, with a
+    // sliver of a last cell layer merged)
+    const frnn_plan_t plan = frnn::binning_plan(ref_plan, dim);
     e->has_result = false;
     if (plan.path == FRNN_PATH_EMPTY) {
         e->has_result = true;

@@ -79,6 +79,29 @@ inline long long grid_cells(int N, int D, const frnn_plan_t& p) {
     return p.cells;
 }
 FrameLayout frame_layout(int N, int D, long long cells);
+
+// The grid the device pipeline bins on.  Raw grids (no frame) cover the
+// reference's [0, 1] domain with res = ceil(1/r) cells of edge r per axis.
+// When 1/r lies just above an integer, the last layer of cells,
+// [(res-1) r, 1], is a sliver: its rows hold a few points spread along the
+// whole row, and every such row becomes a segment of the search that streams
+// three full neighbouring rows.  Binning clamps into the edge cells, which
+// every pruning test treats as unbounded outward, so merging a sliver
+// thinner than half a cell into the layer before it (res - 1 cells per axis,
+// the last one wider than r) keeps every pair within the radius in adjacent
+// cells.  Framed plans and all other grids are returned unchanged.
+inline frnn_plan_t binning_plan(const frnn_plan_t& p, int D) {
+    if ((p.path != FRNN_PATH_GRID_FULL && p.path != FRNN_PATH_GRID_FIRST) || has_frame(p, D) || p.res < 4)
+        return p;
+    const double r = p.cell_size;
+    if ((double)(p.res - 1) * r < 1.0 - 0.5 * r) return p;
+    frnn_plan_t q = p;
+    q.res = p.res - 1;
+    long long c = 1;
+    for (int d = 0; d < p.grid_dim; ++d) c *= q.res;
+    q.cells = c;
+    return q;
+}
 // Frame of a first-coordinate plan: terms, sampled covariance, principal
 // directions, grid and sub-bin geometry.  Needs the point statistics.
 int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long long cells,

@@ -83,6 +83,35 @@ def test_out_of_domain_points_are_clamped_not_dropped():
         assert same.mean() > 0.999   # grid shell == brute force except fp-order ties at r
 
 
+@pytest.mark.parametrize("D,r", [(3, 0.02629), (2, 0.0101), (3, 0.05)])
+def test_sliver_last_cell_layer(D, r):
+    # 1/r just above an integer: the last cell layer [(res-1) r, 1] is a
+    # sliver that the device grid merges into the layer before it (r = 0.05:
+    # no sliver, the reference's grid unchanged); points at x == 1.0 and past
+    # the domain exercise the merged, unbounded edge cells
+    rs = np.random.RandomState(5)
+    X = rs.rand(20000, D).astype(np.float32)
+    X[:50, 0] = 1.0
+    X[50:100] = rs.uniform(0.97, 1.03, (50, D)).astype(np.float32)
+    log(f"sliver D={D} r={r}")
+    gi, gd, plan = engine_search(X, 16, r)
+    assert plan["path"] == "grid_full"
+    ri, rd = O.search(X, 16, r)
+    assert_rows_equal(gi, gd, ri, rd, f"sliver D={D} r={r}")
+
+
+def test_reference_sweep_cell_sampled():
+    # a cell of the reference's own published sweep (its generator, radius
+    # and K = 16), sampled rows against the oracle over the full database
+    w = W.config("refD16N200000")
+    log(f"reference sweep cell: N={w.N} D={w.D} K={w.K} r={w.radius}")
+    gi, gd, plan = engine_search(w.X, w.K, w.radius)
+    assert plan["path"] == "grid_first"
+    q = _sample_queries(w.N, 1000)
+    ri, rd = O.search(w.X, w.K, w.radius, query_ids=q)
+    assert_rows_equal(gi[q], gd[q], ri, rd, "refD16N200000 sampled")
+
+
 def test_nan_points_have_no_neighbours():
     rs = np.random.RandomState(6)
     X = rs.rand(2000, 16).astype(np.float32)
