@@ -15,9 +15,12 @@ __host__ __device__ inline int aos_stride(int D) {
 }
 
 // Per-query candidate list entries: K kept after a compaction, room for a full
-// 64-entry recheck batch and at least 64 more arrivals between compactions.
-// At most 256, the largest register sort of the search kernel.
-inline int list_capacity(int K) { return K + 128; }
+// 64-entry recheck batch and at least 32 more arrivals between compactions; at
+// least 160 (a compaction once a list holds more than 96 keys), which measured
+// fastest at K = 32 and 64: earlier compactions tighten the query's threshold
+// sooner, later ones sort less often.  At most 256, the largest register
+// sort of the search kernel.
+inline int list_capacity(int K) { return K + 96 > 160 ? K + 96 : 160; }
 
 int scan_partials_count(int n);
 
