@@ -207,7 +207,9 @@ void search_kernel(SearchArgs a) {
     __shared__ int t_pos[32];
     __shared__ int t_idx[kTileExact ? 32 : 1];
     __shared__ __align__(16) float t_rows[kStageRows ? 32 * RS : 4];
-    __shared__ unsigned short s_hit[kTileExact ? 32 * 32 : 2];
+    // (a tile holds at most 32 x 32 hits; 64 more entries take the writes of
+    // lanes without a hit, one per lane)
+    __shared__ unsigned short s_hit[kTileExact ? 32 * 32 + kWave : 2];
     // grid geometry per axis (cells, cell-id stride, origin), the segment's
     // bounding box and row coordinates, and each query's grid coordinates
     __shared__ int s_res[kMaxG], s_stride[kMaxG];
@@ -568,23 +570,27 @@ void search_kernel(SearchArgs a) {
         const bool fast = __ballot(!whole) == 0;
         const bool take = width != 0;
         int total = 0;
-        auto push = [&](int r, bool hr) __attribute__((always_inline)) {
-            const unsigned long long m = __ballot(hr);
-            if (m) {
-                if (hr) {
-                    const int off = total + (int)__builtin_amdgcn_mbcnt_hi(
-                                                (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
-                    s_hit[off] = (unsigned short)(((8 * (r >> 2) + (r & 3)) << 5) + lane_code);
-                }
-                total += __popcll(m);
-            }
+        // every lane writes (no branch): a hit at its ballot prefix offset,
+        // a non-hit to its own slot past the hit entries.  m is the mask of
+        // the register's hits (each condition a single compare, combined in
+        // scalar registers).
+        auto push = [&](int r, unsigned long long m) __attribute__((always_inline)) {
+            const bool hr = __builtin_amdgcn_inverse_ballot_w64(m);
+            const int pre = (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+            s_hit[hr ? total + pre : 32 * 32 + lane] = (unsigned short)(((8 * (r >> 2) + (r & 3)) << 5) + lane_code);
+            total += __popcll(m);
         };
         if (fast) {
+            const unsigned long long tk = __builtin_amdgcn_ballot_w64(take);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) push(r, take && !(acc[r] >= thr_f));
+            for (int r = 0; r < 16; ++r) push(r, __builtin_amdgcn_ballot_w64(!(acc[r] >= thr_f)) & tk);
         } else {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) push(r, hit_in(acc, r, first, width));
+            for (int r = 0; r < 16; ++r) {
+                const int rowlo = 8 * (r >> 2) + (r & 3);
+                push(r, __builtin_amdgcn_ballot_w64(!(acc[r] >= thr_f)) &
+                            __builtin_amdgcn_ballot_w64((unsigned)(rowlo - first) < (unsigned)width));
+            }
         }
         bump(1, total);
         if (total == 0) return;
