@@ -162,12 +162,13 @@ __device__ __forceinline__ float exact_d2(const float* q, const float* __restric
 }
 
 // Rows of up to 16 floats keep four waves per SIMD resident (register budget
-// 128; the search is bound by the latency of its gathers, list round trips
-// and sorts, so the extra wave outweighs a few spilled registers), larger ones
-// two (256 VGPRs + AGPRs), so a second wave's MFMA chain can overlap one
-// wave's hit handling.
+// 128), rows of 4 five (96): the search is bound by the latency of its
+// gathers, list round trips and sorts, so the extra wave outweighs a few
+// spilled registers (measured: DS = 4 fastest at five, DS = 12 and 16 at four).
+// Larger rows keep two (256 VGPRs + AGPRs), so a second wave's MFMA chain can
+// overlap one wave's hit handling.
 template <int DS>
-struct WavesPerEU { static constexpr int value = DS <= 16 ? 4 : 2; };
+struct WavesPerEU { static constexpr int value = DS <= 4 ? 5 : DS <= 16 ? 4 : 2; };
 
 // CNT: the profiling build of the kernel, which also keeps the work counters
 // (a separate instantiation, so the counting code costs the plain kernel no
