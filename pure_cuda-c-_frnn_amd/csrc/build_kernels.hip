@@ -192,14 +192,34 @@ __global__ __launch_bounds__(256) void dim_stats_kernel(const float* __restrict_
     const double pivot = col[0];
     double sum = 0.0, sq = 0.0;
     float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
-    for (long long i = (long long)blockIdx.x * 256 + t; i < N; i += 256LL * gridDim.x) {
-        const float v = col[i];
+    auto take = [&](float v) __attribute__((always_inline)) {
         const double dv = (double)v - pivot;
         sum += dv;
         sq += dv * dv;
         mn = fminf(mn, v);
         mx = fmaxf(mx, v);
+    };
+    // 16-byte loads, four per thread in flight (a column is 16-byte aligned
+    // when d * N is a multiple of 4); the block's slices interleave at 1 KB
+    const bool vec = ((reinterpret_cast<uintptr_t>(col) & 15) == 0);
+    const long long n4 = vec ? N / 4 : 0;
+    const float4* col4 = reinterpret_cast<const float4*>(col);
+    const long long step = 256LL * gridDim.x;
+    long long j = (long long)blockIdx.x * 256 + t;
+    for (; j + 3 * step < n4; j += 4 * step) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = col4[j + u * step];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            take(v[u].x); take(v[u].y); take(v[u].z); take(v[u].w);
+        }
     }
+    for (; j < n4; j += step) {
+        const float4 v = col4[j];
+        take(v.x); take(v.y); take(v.z); take(v.w);
+    }
+    for (long long i = 4 * n4 + (long long)blockIdx.x * 256 + t; i < N; i += step) take(col[i]);
     s_sum[t] = sum; s_sq[t] = sq; s_mn[t] = mn; s_mx[t] = mx;
     __syncthreads();
     for (int o = 128; o > 0; o >>= 1) {
