@@ -167,51 +167,45 @@ __device__ __forceinline__ void wave_bitonic_merge_u64(unsigned long long (&x)[E
     for (int lj = log2_keys<E>() - 1; lj >= 0; --lj) bitonic_step<E>(x, 0, 1 << lj);
 }
 
-// Wave-wide reductions over the VALU lane exchanges above.
-__device__ __forceinline__ int wave_min_i32(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        unsigned p, q;
-        xor_pair_u32((unsigned)v, o, p, q);
-        v = min((int)p, (int)q);
-    }
+// Wave-wide reductions over the VALU lane exchanges above (the six steps are
+// spelled out: a loop over the distance was left rolled by the compiler in
+// places, with a run-time dispatch on every step).
+template <class Op>
+__device__ __forceinline__ unsigned wave_reduce_u32(unsigned v, Op op) {
+    unsigned p, q;
+    xor_pair_u32(v, 32, p, q); v = op(p, q);
+    xor_pair_u32(v, 16, p, q); v = op(p, q);
+    xor_pair_u32(v, 8, p, q); v = op(p, q);
+    xor_pair_u32(v, 4, p, q); v = op(p, q);
+    xor_pair_u32(v, 2, p, q); v = op(p, q);
+    xor_pair_u32(v, 1, p, q); v = op(p, q);
     return v;
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    return (int)wave_reduce_u32((unsigned)v, [](unsigned p, unsigned q) { return (unsigned)min((int)p, (int)q); });
 }
 __device__ __forceinline__ int wave_max_i32(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        unsigned p, q;
-        xor_pair_u32((unsigned)v, o, p, q);
-        v = max((int)p, (int)q);
-    }
-    return v;
+    return (int)wave_reduce_u32((unsigned)v, [](unsigned p, unsigned q) { return (unsigned)max((int)p, (int)q); });
 }
 __device__ __forceinline__ float wave_min_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        unsigned p, q;
-        xor_pair_u32(__float_as_uint(v), o, p, q);
-        v = fminf(__uint_as_float(p), __uint_as_float(q));
-    }
-    return v;
+    return __uint_as_float(wave_reduce_u32(__float_as_uint(v), [](unsigned p, unsigned q) {
+        return __float_as_uint(fminf(__uint_as_float(p), __uint_as_float(q)));
+    }));
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        unsigned p, q;
-        xor_pair_u32(__float_as_uint(v), o, p, q);
-        v = fmaxf(__uint_as_float(p), __uint_as_float(q));
-    }
-    return v;
+    return __uint_as_float(wave_reduce_u32(__float_as_uint(v), [](unsigned p, unsigned q) {
+        return __float_as_uint(fmaxf(__uint_as_float(p), __uint_as_float(q)));
+    }));
 }
 __device__ __forceinline__ long long wave_sum_i64(long long v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        unsigned long long p, q;
-        xor_pair_u64((unsigned long long)v, o, p, q);
-        v = (long long)(p + q);
-    }
-    return v;
+    unsigned long long x = (unsigned long long)v, p, q;
+    xor_pair_u64(x, 32, p, q); x = p + q;
+    xor_pair_u64(x, 16, p, q); x = p + q;
+    xor_pair_u64(x, 8, p, q); x = p + q;
+    xor_pair_u64(x, 4, p, q); x = p + q;
+    xor_pair_u64(x, 2, p, q); x = p + q;
+    xor_pair_u64(x, 1, p, q); x = p + q;
+    return (long long)x;
 }
 
 }  // namespace frnn
