@@ -458,7 +458,7 @@ void search_kernel(SearchArgs a) {
         float op[HD];
         int pos, count;
         int v0;                         // stream position of row 0
-        int idx;                        // original index (tile-exact path, h == 0 lanes)
+        int idx;                        // original index (tile-exact path)
     };
     auto gather = [&](int v0, int count, Tile& t) __attribute__((always_inline)) {
         const int v = v0 + n;
@@ -473,7 +473,9 @@ void search_kernel(SearchArgs a) {
             const int j = jr & (kRing - 1);
             t.pos = r_start[j] + (v - r_vbeg[j]);
             if constexpr (kTileExact) {
-                if (h == 0) t.idx = BF ? t.pos : a.sorted_idx[t.pos];
+                // both halves of the wave load it (the same address: one
+                // coalesced access, and no per-half exec mask in the tile loop)
+                t.idx = BF ? t.pos : a.sorted_idx[t.pos];
             }
         }
         const float* pr = op_rows + (size_t)t.pos * DS + h * HD;
@@ -489,7 +491,8 @@ void search_kernel(SearchArgs a) {
     // The norm column |p'|^2 is summed here from the row halves of lanes n and
     // n + 32 (the filter's rounding bound holds for any summation order of the
     // norm), which saves a random 4-byte load per candidate row; rows past the
-    // tile read as far away.  cand_norm returns the norm on h == 0 lanes.
+    // tile read as far away.  cand_norm returns the norm (the same on both
+    // halves of the wave).
     auto mfma_tile = [&](const Tile& t, float& cand_norm) __attribute__((always_inline)) {
         floatx16 acc;
 #pragma unroll
@@ -550,13 +553,12 @@ void search_kernel(SearchArgs a) {
     // prefix offsets, and they are re-evaluated in rounds of 64 lanes, each
     // round preceded by the compaction of any list that could overflow in it.
     auto hits_tile_exact = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
-        const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
+        const bool robust = robust_q || (__ballot(n < t.count && !(cand_norm < 1.0e37f)) != 0);
         if (!any_hit(acc, robust)) return;
         lds_sync();
-        if (h == 0) {
-            t_pos[n] = t.pos;
-            t_idx[n] = t.idx;
-        }
+        // both halves store the same values
+        t_pos[n] = t.pos;
+        t_idx[n] = t.idx;
         if constexpr (kStageRows) {
             float* dst = t_rows + n * RS + h * HD;
 #pragma unroll
@@ -638,7 +640,7 @@ void search_kernel(SearchArgs a) {
     // exact batches run after, when the accumulator registers are no longer
     // live.
     auto hits_queue = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
-        const bool robust = robust_q || (__ballot(h == 0 && n < t.count && !(cand_norm < 1.0e37f)) != 0);
+        const bool robust = robust_q || (__ballot(n < t.count && !(cand_norm < 1.0e37f)) != 0);
         // hits are sparse here: first find the groups of four registers that
         // might hold one
         bool gh[4];
