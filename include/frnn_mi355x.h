@@ -80,7 +80,7 @@ typedef struct frnn_dim_stat {
  * grid directions are orthonormal up to a 2^-18 shrink); margin bounds |computed -
  * exact projection| over every finite input point.  Directions 0..grid_dim-1 are
  * the grid axes: cell coordinate c_k = clamp(floor((s_k - lo[k]) * inv_h), 0,
- * res[k] - 1) and cell id sum_k c_k * stride[k].  Directions 4 and 5 order the
+ * res[k] - 1) (inv_h0 for k = 0) and cell id sum_k c_k * stride[k].  Directions 4 and 5 order the
  * points inside cells of >= 256 points: sub-bin clamp(floor((s - rlo) * rinv),
  * 0, bins - 1).  projected == 0 (infinite input) falls back to the first
  * grid_dim raw coordinates with the plan's cell size and resolution. */
@@ -93,7 +93,7 @@ typedef struct frnn_frame {
     int axes;              /* refinement directions (0, 1 or 2) */
     int projected;         /* 1: principal directions; 0: raw first coordinates */
     int bins0, bins1;      /* refinement sub-bins per direction; bins0 * bins1 == 1024 */
-    int reserved0;
+    int fine0;             /* cells of direction 0 per cell edge h (its cells are h / fine0 wide) */
     int res[4];            /* cells per grid direction */
     int stride[4];         /* cell-id stride per grid direction, stride[0] == 1 */
     float lo[4];           /* grid origin per direction */
@@ -103,7 +103,7 @@ typedef struct frnn_frame {
     float rlo0, rlo1;      /* refinement bin origin per direction */
     float rinv0, rinv1;    /* refinement bins per unit (0: a single bin) */
     float sigma[6];        /* standard deviation of the projections per direction */
-    int reserved1[2];
+    float h0, inv_h0;      /* direction 0's cell edge h / fine0 and fl(1/h0) */
     int coord[FRNN_FRAME_TERMS];               /* term coordinates, highest variance first */
     float mean[FRNN_FRAME_TERMS];              /* term centres (the point-statistics means) */
     float dir[FRNN_FRAME_DIRS][FRNN_FRAME_TERMS];   /* 0..3 grid, 4..5 refinement */

@@ -275,7 +275,7 @@ __global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restric
 // non-finite bound (infinite input) is stored as +inf; frame_dirs_kernel then
 // falls back to the raw first coordinates.
 __global__ __launch_bounds__(128) void frame_terms_kernel(const DimStat* __restrict__ st, int g, int D,
-                                                          Frame* __restrict__ f) {
+                                                          int fine0, Frame* __restrict__ f) {
     __shared__ float s_var[FRNN_MAX_DIM];
     __shared__ int s_coord[kMaxTerms];
     const int tid = threadIdx.x;
@@ -312,8 +312,10 @@ __global__ __launch_bounds__(128) void frame_terms_kernel(const DimStat* __restr
     }
     f->g = g;
     f->terms = T;
-    const int m = (g + 2 < T) ? g + 2 : T;   // grid + refinement directions
-    f->L = m - g;
+    // grid + refinement directions (none with a fine axis 0, which orders
+    // the points inside cells instead)
+    const int m = (g + 2 < T && fine0 == 1) ? g + 2 : (g < T ? g : T);
+    f->L = m > g ? m - g : 0;
     f->nb1 = f->L == 2 ? 32 : kSubBins;
     f->nb2 = f->L == 2 ? 32 : 1;
     const double E = (T + 2) * 5.9604644775390625e-08 * sqrt(R2) * (1.0 + 9.765625e-04);
@@ -450,7 +452,8 @@ constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 // cell size.
 __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict__ covsum, double nsamp,
                                                         float radius, float cell_raw, float inv_cell_raw,
-                                                        int res_raw, int cells_cap, Frame* __restrict__ f) {
+                                                        int res_raw, int cells_cap, int fine0,
+                                                        Frame* __restrict__ f) {
     __shared__ double s_C[kMaxTerms][kMaxTerms + 1];   // covariance
     __shared__ double s_A[kMaxTerms][kMaxTerms + 1];   // (C / cmax)^2
     __shared__ double s_P[kMaxTerms][kMaxTerms + 1];   // C / cmax, then (C / cmax)^4
@@ -592,20 +595,24 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     if (t != 0) return;
     // ---- geometry (one thread) ----
     const bool exact = f->margin < 1.0e30f;
+    f->fine0 = fine0;
     if (!exact) {
         // infinite input: grid on the raw first g coordinates, no refinement
+        // (axis 0 still in fine0 cells per plan cell)
         f->projected = 0;
         f->L = 0;
         f->margin = 0.0f;
         f->slack = 0.0f;
         f->h = cell_raw;
         f->inv_h = inv_cell_raw;
+        f->h0 = cell_raw / (float)fine0;         // fine0 is a power of two: exact
+        f->inv_h0 = inv_cell_raw * (float)fine0;
         int stride = 1;
         for (int d = 0; d < kFrameGrid; ++d) {
-            f->res[d] = d < g ? res_raw : 1;
+            f->res[d] = d < g ? (d == 0 ? res_raw * fine0 : res_raw) : 1;
             f->lo[d] = 0.0f;
             f->stride[d] = stride;
-            if (d < g) stride *= res_raw;
+            stride *= f->res[d];
         }
         f->cells = stride;
         f->rlo0 = f->rlo1 = f->rinv0 = f->rinv1 = 0.0f;
@@ -626,7 +633,9 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     double h = fmax(h0 + 2.0 * slack, 8.0 * smax / 1048576.0);
     int res[kFrameGrid];
     long long cells = 0;
-    for (int pass = 0; pass < 4096 && !(cells >= 1 && cells <= cells_cap); ++pass) {
+    // the cells of edge h fit cells_cap / fine0; axis 0 is then split fine0 ways
+    const long long coarse_cap = cells_cap / fine0;
+    for (int pass = 0; pass < 4096 && !(cells >= 1 && cells <= coarse_cap); ++pass) {
         if (pass > 0) h *= 1.0625;
         cells = 1;
         for (int d = 0; d < kFrameGrid; ++d) {
@@ -636,8 +645,9 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
             cells *= res[d];
         }
     }
-    if (!(cells >= 1 && cells <= cells_cap))
+    if (!(cells >= 1 && cells <= coarse_cap))
         for (int d = 0; d < kFrameGrid; ++d) res[d] = 1;
+    if (g >= 1) res[0] *= fine0;
     // store h rounded up and inv_h rounded down, so the binning never
     // narrows a cell below h
     // (both positive: one ulp up / down is the bit pattern +- 1)
@@ -647,6 +657,9 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     if ((double)ih > 1.0 / (double)hf) ih = __uint_as_float(__float_as_uint(ih) - 1u);
     f->h = hf;
     f->inv_h = ih;
+    // axis 0: fine0 (a power of two) cells per h, exact scalings of h, inv_h
+    f->h0 = hf / (float)fine0;
+    f->inv_h0 = ih * (float)fine0;
     f->slack = (float)slack;
     int stride = 1;
     for (int d = 0; d < kFrameGrid; ++d) {
@@ -693,7 +706,7 @@ __global__ __launch_bounds__(256) void bin_frame_kernel(const float* __restrict_
     int c = 0;
 #pragma unroll
     for (int d = 0; d < kFrameGrid; ++d)
-        if (d < g) c += sub_bin(s[d], f->lo[d], f->inv_h, f->res[d]) * f->stride[d];
+        if (d < g) c += sub_bin(s[d], f->lo[d], d == 0 ? f->inv_h0 : f->inv_h, f->res[d]) * f->stride[d];
     c = c < cells ? c : cells - 1;   // the frame fits `cells`; a mismatched count array stays in bounds
     cell_of[i] = c;
     rank[i] = atomicAdd(&cnt[c], 1);
@@ -920,7 +933,7 @@ int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long l
     Frame* f = reinterpret_cast<Frame*>(base + L.frame);
     const DimStat* st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
     double* cov = reinterpret_cast<double*>(base + L.cov);
-    hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(128), 0, s, st, plan.grid_dim, D, f);
+    hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(128), 0, s, st, plan.grid_dim, D, kFine0, f);
     // covariance sample: kCovBlocks tiles of 256 consecutive points, evenly spaced
     const long long tile_stride = N <= (long long)kCovBlocks * 256 ? 256 : (long long)N / kCovBlocks;
     long long nsamp = 0;
@@ -932,7 +945,7 @@ int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long l
     hipLaunchKernelGGL(cov_kernel, dim3(kCovBlocks), dim3(256), 0, s, pts, N, tile_stride, f, cov);
     hipLaunchKernelGGL(cov_reduce_kernel, dim3(kMaxPairs), dim3(256), 0, s, cov, kCovBlocks, f, covsum);
     hipLaunchKernelGGL(frame_dirs_kernel, dim3(1), dim3(kWave), 0, s, covsum, (double)nsamp,
-                       plan.cell_size, plan.cell_size, plan.inv_cell, plan.res, (int)cells, f);
+                       plan.cell_size, plan.cell_size, plan.inv_cell, plan.res, (int)cells, kFine0, f);
     return launch_result();
 }
 

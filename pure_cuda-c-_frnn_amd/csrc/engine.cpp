@@ -197,8 +197,10 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
         ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)cells + 1, e->start, e->partials, s),
                              "scan launch"));
     ST_TRY(mark(5));
-    // stage 5: within-cell refinement of big cells (framed plans)
-    if (framed)
+    // stage 5: within-cell refinement of big cells: none (a frame orders the
+    // points of a cell by its fine axis 0 instead)
+    const bool refined = framed && frnn::kFine0 == 1;
+    if (refined)
         ST_TRY(launch_status(frnn::launch_refine(d_pts, N, dim, cells, e->cell_of, e->cnt, e->rank,
                                                  e->frame_ws, s),
                              "refinement launch"));
@@ -207,7 +209,8 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     // brute force, the AoS copy
     if (grid)
         ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start, e->cnt,
-                                                  frame, cells, e->sorted_idx, e->inv, e->aos, e->stats_ws,
+                                                  refined ? frame : nullptr, cells, e->sorted_idx, e->inv,
+                                                  e->aos, e->stats_ws,
                                                   frows, s),
                              "reorder launch"));
     else
@@ -340,7 +343,8 @@ int frnn_engine_create(int max_points, frnn_engine_t** out) {
     frnn_engine* e = new frnn_engine();
     e->max_p = max_points;
     const size_t P = (size_t)max_points;
-    const size_t C = (size_t)FRNN_MAX_CELLS + 1;
+    // count arrays hold a frame's cells (kFine0 x the raw cap) + 1
+    const size_t C = (size_t)frnn::kFine0 * FRNN_MAX_CELLS + 1;
     hipError_t err = hipSuccess;
     auto alloc = [&](void** p, size_t bytes) {
         if (err == hipSuccess) err = hipMalloc(p, bytes);
@@ -486,7 +490,8 @@ long long frnn_grid_cells(int N, int dim, const frnn_plan_t* plan) {
 
 int frnn_launch_bin_count(const float* d_pts, int N, int grid_dim, int res, float inv_cell, long long cells,
                           const void* d_frame_ws, int* d_cell_of, int* d_rank, int* d_cnt, void* stream) {
-    if (N < 0 || grid_dim < 1 || grid_dim > 9 || res < 1 || cells < 1 || cells > FRNN_MAX_CELLS)
+    if (N < 0 || grid_dim < 1 || grid_dim > 9 || res < 1 || cells < 1 ||
+        cells > (d_frame_ws ? (long long)frnn::kFine0 * FRNN_MAX_CELLS : FRNN_MAX_CELLS))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "bad bin/count geometry");
     if (!d_frame_ws && ipow_sat(res, grid_dim, (long long)4e18) != cells)
         return fail(FRNN_ERR_INVALID_ARGUMENT, "cells must equal res^grid_dim");
@@ -567,7 +572,7 @@ int frnn_launch_reorder(const float* d_pts, int N, int dim, const int* d_cell_of
     if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
     if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_start || !d_sorted_idx || !d_inv || !d_sorted_aos))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    if (d_frame_ws && (!d_cnt || cells < 1 || cells > FRNN_MAX_CELLS))
+    if (d_frame_ws && (!d_cnt || cells < 1 || cells > (long long)frnn::kFine0 * FRNN_MAX_CELLS))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame needs the counts and the cell count");
     if (d_frows && !d_stats_ws) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need the statistics");
     return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_cnt, d_frame_ws,

@@ -43,14 +43,14 @@ constexpr int kRefDir0 = 4;             // refinement directions (slots 4, 5)
 struct Frame {
     int g, cells, terms, L;             // grid directions, cells, projection terms, refinement dirs
     int projected;                      // 0: raw first coordinates (infinite input)
-    int nb1, nb2, reserved0;            // refinement sub-bins per direction
+    int nb1, nb2, fine0;                // refinement sub-bins per direction; cells of axis 0 per h
     int res[kFrameGrid];
     int stride[kFrameGrid];
     float lo[kFrameGrid];
     float h, inv_h, margin, slack;
     float rlo0, rlo1, rinv0, rinv1;
     float sigma[FRNN_FRAME_DIRS];
-    int reserved1[2];
+    float h0, inv_h0;                   // axis 0's cell edge h / fine0 and fl(1/h0)
     int coord[kMaxTerms];
     float mean[kMaxTerms];
     float dir[FRNN_FRAME_DIRS][kMaxTerms];
@@ -71,13 +71,19 @@ StatsLayout stats_layout(int D);
 int launch_point_stats(const float* pts, int N, int D, void* stats_ws, hipStream_t s);
 
 inline bool has_frame(const frnn_plan_t& p, int D) { return p.path == FRNN_PATH_GRID_FIRST && D > p.grid_dim; }
+// A frame's axis 0 has kFine0 cells per cell edge h: points are ordered by
+// their projection on it inside every row of cells, so a chunk of queries
+// covers a short stretch of its row and the search streams only the stretch
+// of each neighbouring row within reach of the chunk (all other grid axes keep
+// cells of edge h, so the rows, and the query runs sharing one, stay as long).
+constexpr int kFine0 = 8;
 // Cells (count array length - 1) of a grid plan: res^g, or the frame's
-// capacity (at least res^g, which its raw-coordinate fallback uses).
+// capacity: kFine0 x (at least res^g, which its raw-coordinate fallback uses).
 inline long long grid_cells(int N, int D, const frnn_plan_t& p) {
     if (has_frame(p, D)) {
         long long c = N < 4096 ? 4096 : N;
         c = c < FRNN_MAX_CELLS ? c : FRNN_MAX_CELLS;
-        return c > p.cells ? c : p.cells;
+        return (c > p.cells ? c : p.cells) * kFine0;
     }
     return p.cells;
 }

@@ -757,38 +757,36 @@ void search_kernel(SearchArgs a) {
     } else {
         // Grid geometry: the frame's projected axes (first-coordinate plans)
         // or the raw coordinates on the plan's cells.  Cell ci of axis d spans
-        // [org_d + ci h, org_d + (ci + 1) h]; the binned values of its points
-        // lie within slack of that span (edge cells are unbounded outward, as
-        // binning clamps) and within margin of the exact projections, so the
-        // per-axis gaps below shrink by slack + 2 margin (0 on raw grids).
-        // Frame directions have norm < 1 and are orthonormal up to a shrink,
-        // so the gaps lower-bound the distance.
+        // [org_d + ci h_d, org_d + (ci + 1) h_d]; the binned values of its
+        // points lie within slack of that span (edge cells are unbounded
+        // outward, as binning clamps) and within margin of the exact
+        // projections, so the per-axis gaps below shrink by slack + 2 margin
+        // (0 on raw grids).  Frame directions have norm < 1 and are
+        // orthonormal up to a shrink, so the gaps lower-bound the distance.
         const Frame* fr = a.frame;
         const bool proj = fr != nullptr && fr->projected != 0;
         const int G = a.G;
         const int res0 = fr ? fr->res[0] : a.res;
         const float gh = fr ? fr->h : a.cell;
+        const float gh0 = fr ? fr->h0 : a.cell;
+        const float ginv0 = fr ? fr->inv_h0 : 0.0f;
+        const int fine0 = fr ? fr->fine0 : 1;
         const float gsm = fr ? fr->slack + 2.0f * fr->margin : 0.0f;
-        const int L = fr ? fr->L : 0;
         if (lane < G) {
             s_res[lane] = fr ? fr->res[lane] : a.res;
             s_stride[lane] = fr ? fr->stride[lane] : a.gstride[lane];
             s_org[lane] = fr ? fr->lo[lane] : 0.0f;
         }
-        // this lane's query: grid coordinates (projections or raw values) and
-        // its projections onto the refinement directions
+        // this lane's query: grid coordinates (projections or raw values)
         const float* qrow = query_row(qvalid ? n : 0);
-        float pj0 = 0.0f, pj1 = 0.0f;
         if (proj) {
-            float sp[FRNN_FRAME_DIRS];
+            float sp[kFrameGrid];
             frame_project(fr, 0, [&](int d) { return qrow[d]; }, sp);
             if (h == 0) {
 #pragma unroll
                 for (int d = 0; d < kFrameGrid; ++d)
                     if (d < G) s_qg[n * kGA + d] = sp[d];
             }
-            pj0 = sp[kRefDir0];
-            pj1 = sp[kRefDir0 + 1];
         } else if (h == 0) {
             for (int d = 0; d < G; ++d) s_qg[n * kGA + d] = qrow[d];
         }
@@ -810,13 +808,14 @@ void search_kernel(SearchArgs a) {
         auto axis_gap = [&](int d, int ci) __attribute__((always_inline)) -> float {
             float gap = 0.0f;
             const float org = s_org[d];
+            const float hd = d == 0 ? gh0 : gh;
             if (ci > 0) {
-                const float lo = fmaf((float)ci, gh, org);
+                const float lo = fmaf((float)ci, hd, org);
                 const float bh = s_bhi[d];
                 gap = fmaxf(gap, (lo - bh) - eps * (fabsf(lo) + fabsf(bh)));
             }
             if (ci < s_res[d] - 1) {
-                const float hi = fmaf((float)(ci + 1), gh, org);
+                const float hi = fmaf((float)(ci + 1), hd, org);
                 const float bl = s_blo[d];
                 gap = fmaxf(gap, (bl - hi) - eps * (fabsf(hi) + fabsf(bl)));
             }
@@ -824,19 +823,15 @@ void search_kernel(SearchArgs a) {
         };
 
         // One loop walks the segments (runs of queries sharing a row) and, per
-        // segment, batches of 64 cells (one per lane); every iteration appends
+        // segment, batches of 64 items (one per lane); every iteration appends
         // at most one run per lane and streams what is available, so the tile
-        // loop below is inlined once.  A refined cell whose window is narrower
-        // than the cell contributes one run per sub-bin row of the window, over
-        // successive iterations of the same batch.
+        // loop below is inlined once.  Items: on a frame, the 3^(g-1)
+        // neighbouring rows, each contributing the stretch of its fine axis-0
+        // cells within reach of the segment (one contiguous run); on a raw
+        // grid, the cells x-1..x+1 around the segment's queries in those rows.
         int seg = 0;
         int ib = 0, NI = 0;
-        int kk = 0, kmax = 0;               // sub-run index within the batch (wave-uniform)
-        int xa = 0, nx = 1, nq1 = 1, qlo0 = 0, qlo1 = 0, qhi1 = 0, nb2 = 1;
-        bool windowed = false;              // the segment's window excludes some sub-bins
-        // this lane's cell of the current batch: cell id, sorted range, and the
-        // number of runs it contributes (0, 1, or nq1 for a windowed big cell)
-        int c_cell = 0, c_start = 0, c_end = 0, c_runs = 0;
+        int xa = 0, nx = 1;
         float thr_seg = 0.0f;
         bool seg_mine = false;              // this lane's query is in the current segment
         bool last = false;
@@ -857,7 +852,7 @@ void search_kernel(SearchArgs a) {
                 // non-decreasing in the cell-sorted order); at least one step,
                 // so every wave terminates even on unsorted input
                 seg = max(seg + 1, (int)__popcll(__ballot(row_n <= R) & 0xffffffffull));
-                // segment bounding box on the grid axes and the largest threshold
+                // segment bounding box on the grid axes
                 for (int d = 0; d < G; ++d) {
                     const float qd = s_qg[n * kGA + d];
                     const float lo = wave_min_f32(in_seg ? qd : __builtin_huge_valf());
@@ -868,37 +863,17 @@ void search_kernel(SearchArgs a) {
                         s_rc[d] = d > 0 ? (R / s_stride[d]) % s_res[d] : 0;
                     }
                 }
-                // refinement windows: a candidate within the radius of a segment
-                // query q has |s(p) - s(q)| <= |p - q| + 2 margin on each direction
-                // (weights of norm < 1), so its projection lies in [lo - h, hi + h]
-                // over the segment's projections; h adds the fp32 distance slack
-                // (2^-15 relative) and the rounding of the window ends (2^-22 of
-                // |lo| + |hi|).  sub_bin is monotone, so the window is a sub-bin range.
-                int qhi0 = 0;
-                qlo0 = qlo1 = qhi1 = 0;
-                nb2 = 1;
-                if (L > 0) {
-                    nb2 = fr->nb2;
-                    const float hw = a.radius * 1.000030517578125f + 2.0f * fr->margin;
-                    const float lo0 = wave_min_f32(in_seg ? pj0 : __builtin_huge_valf());
-                    const float hi0 = wave_max_f32(in_seg ? pj0 : -__builtin_huge_valf());
-                    const float h0 = hw + 2.384185791015625e-07f * (fabsf(lo0) + fabsf(hi0));
-                    qlo0 = sub_bin(lo0 - h0, fr->rlo0, fr->rinv0, fr->nb1);
-                    qhi0 = sub_bin(hi0 + h0, fr->rlo0, fr->rinv0, fr->nb1);
-                    if (L > 1) {
-                        const float lo1 = wave_min_f32(in_seg ? pj1 : __builtin_huge_valf());
-                        const float hi1 = wave_max_f32(in_seg ? pj1 : -__builtin_huge_valf());
-                        const float h1 = hw + 2.384185791015625e-07f * (fabsf(lo1) + fabsf(hi1));
-                        qlo1 = sub_bin(lo1 - h1, fr->rlo1, fr->rinv1, fr->nb2);
-                        qhi1 = sub_bin(hi1 + h1, fr->rlo1, fr->rinv1, fr->nb2);
-                    }
-                }
                 lds_sync();
 
                 if constexpr (counting) {
-                    // the reference's shell candidates of this segment's queries
+                    // the reference's shell candidates of this segment's queries:
+                    // the cells x-1..x+1 of edge h (fine0 axis-0 cells each) in
+                    // the 3^(g-1) rows
                     long long sh = 0;
                     if (in_seg && h == 0) {
+                        const int xc = x_n / fine0;
+                        const int f0 = max(xc - 1, 0) * fine0;
+                        const int f1 = min((xc + 2) * fine0, res0) - 1;
                         for (int t = 0; t < nrows; ++t) {
                             int tt = t, Rb = 0;
                             bool ok = true;
@@ -909,79 +884,73 @@ void search_kernel(SearchArgs a) {
                                 Rb += cc * s_stride[d];
                             }
                             if (!ok) continue;
-                            sh += a.start[Rb + min(x_n + 1, res0 - 1) + 1] - a.start[Rb + max(x_n - 1, 0)];
+                            sh += a.start[Rb + f1 + 1] - a.start[Rb + f0];
                         }
                     }
                     bump(0, (unsigned long long)wave_sum_i64(sh));
                 }
 
                 xa = max(xlo - 1, 0);
-                nx = min(xhi + 1, res0 - 1) - xa + 1;
-                nq1 = L > 0 ? max(qhi0 - qlo0 + 1, 0) : 1;
-                windowed = L > 0 && (nq1 < fr->nb1 || qhi1 - qlo1 + 1 < nb2);
+                nx = fr ? 1 : min(xhi + 1, res0 - 1) - xa + 1;
                 NI = nx * nrows;
                 ib = 0;
-                kk = 0;
             }
             if (ib < NI) {
-                if (kk == 0) {
-                    // the segment's largest threshold, as tightened by the
-                    // compactions so far (cells beyond it hold no candidate
-                    // any of its queries would still accept)
-                    thr_seg = wave_max_f32(seg_mine ? key_d2(s_thr[n]) : -__builtin_huge_valf());
-                    // this lane's cell: AABB test against the segment's queries
-                    const int item = ib + lane;
-                    c_runs = 0;
-                    if (item < NI) {
-                        const int x = xa + item % nx;
-                        int tt = natural_row(item / nx, G - 1), Rb = 0;
-                        bool ok = true;
-                        float lb = 0.0f;
-                        {
-                            const float gp = axis_gap(0, x);
-                            lb = gp * gp;
-                        }
-                        for (int d = 1; d < G; ++d) {
-                            const int cc = s_rc[d] + (tt % 3) - 1;
-                            tt /= 3;
-                            const bool in = cc >= 0 && cc < s_res[d];
-                            ok = ok && in;
-                            Rb += cc * s_stride[d];
-                            if (in) {
-                                const float gp = axis_gap(d, cc);
-                                lb = fmaf(gp, gp, lb);
-                            }
-                        }
-                        if (ok) {
-                            c_cell = x + Rb;
-                            c_start = a.start[c_cell];
-                            c_end = a.start[c_cell + 1];
-                            if (c_end > c_start && !(lb * keep > thr_seg))
-                                c_runs = (windowed && c_end - c_start >= kBigCell) ? nq1 : 1;
+                // the segment's largest threshold, as tightened by the
+                // compactions so far (nothing beyond it can still be accepted)
+                thr_seg = wave_max_f32(seg_mine ? key_d2(s_thr[n]) : -__builtin_huge_valf());
+                const int item = ib + lane;
+                int rs = 0, rl = 0;
+                if (item < NI) {
+                    const int x = xa + item % nx;
+                    int tt = natural_row(item / nx, G - 1), Rb = 0;
+                    bool ok = true;
+                    float lb = 0.0f;     // squared gaps on axes 1..g-1
+                    for (int d = 1; d < G; ++d) {
+                        const int cc = s_rc[d] + (tt % 3) - 1;
+                        tt /= 3;
+                        const bool in = cc >= 0 && cc < s_res[d];
+                        ok = ok && in;
+                        Rb += cc * s_stride[d];
+                        if (in) {
+                            const float gp = axis_gap(d, cc);
+                            lb = fmaf(gp, gp, lb);
                         }
                     }
-                    kmax = wave_max_i32(c_runs);
-                }
-                int rs = 0, rl = 0;
-                if (kk < c_runs) {
-                    if (c_runs > 1 || (windowed && c_end - c_start >= kBigCell)) {
-                        // sub-bin row qlo0 + kk of the window, columns qlo1..qhi1
-                        const int q1 = qlo0 + kk;
-                        const size_t sb = (size_t)a.bidx[c_cell] * kSubStride;
-                        const int sl = a.substart[sb + q1 * nb2 + qlo1];
-                        const int sh = a.substart[sb + q1 * nb2 + qhi1 + 1];
-                        rs = c_start + sl;
-                        rl = sh - sl;
-                    } else {
-                        rs = c_start;
-                        rl = c_end - c_start;
+                    if (ok && fr) {
+                        // the row's stretch: a candidate p within the threshold
+                        // of a segment query q has (s0(p) - s0(q))^2 <= |p - q|^2
+                        // - (its gaps on the other axes)^2, and |p - q|^2 < thr
+                        // (1 + 2^-13) for an fp32 distance below thr, so its
+                        // axis-0 projection lies within w of the segment's box
+                        // (w adds sqrt's rounding and slack + 2 margin); binning
+                        // is monotone in the projection, so the stretch is the
+                        // cell range of the window's ends (rounded outward).
+                        if (!(lb * keep > thr_seg)) {
+                            const float w2 = fmaxf(thr_seg * 1.0001220703125f - lb * keep, 0.0f);
+                            const float w = sqrtf(w2) * 1.00000095367431640625f + gsm;
+                            const float bl = s_blo[0], bh = s_bhi[0];
+                            const float wl = (bl - w) - eps * (fabsf(bl) + w);
+                            const float wh = (bh + w) + eps * (fabsf(bh) + w);
+                            const int fx0 = wl == wl ? sub_bin(wl, s_org[0], ginv0, res0) : 0;
+                            const int fx1 = wh == wh ? sub_bin(wh, s_org[0], ginv0, res0) : res0 - 1;
+                            rs = a.start[Rb + fx0];
+                            rl = max(a.start[Rb + fx1 + 1] - rs, 0);
+                        }
+                    } else if (ok) {
+                        const float gp = axis_gap(0, x);
+                        lb = fmaf(gp, gp, lb);
+                        const int c = x + Rb;
+                        const int cs = a.start[c];
+                        const int ce = a.start[c + 1];
+                        if (ce > cs && !(lb * keep > thr_seg)) {
+                            rs = cs;
+                            rl = ce - cs;
+                        }
                     }
                 }
                 append_runs(rs, rl);
-                if (++kk >= kmax) {
-                    kk = 0;
-                    ib += kWave;
-                }
+                ib += kWave;
             }
             last = ib >= NI && seg >= nq;
             consume(last);

@@ -61,13 +61,13 @@ class FrameInfo(ctypes.Structure):
     """frnn_frame_t: the descriptor at the start of a frame workspace."""
     _fields_ = [("grid_dim", ctypes.c_int), ("cells", ctypes.c_int), ("terms", ctypes.c_int),
                 ("axes", ctypes.c_int), ("projected", ctypes.c_int), ("bins0", ctypes.c_int),
-                ("bins1", ctypes.c_int), ("reserved0", ctypes.c_int),
+                ("bins1", ctypes.c_int), ("fine0", ctypes.c_int),
                 ("res", ctypes.c_int * FRAME_GRID), ("stride", ctypes.c_int * FRAME_GRID),
                 ("lo", ctypes.c_float * FRAME_GRID), ("h", ctypes.c_float), ("inv_h", ctypes.c_float),
                 ("margin", ctypes.c_float), ("slack", ctypes.c_float),
                 ("rlo0", ctypes.c_float), ("rlo1", ctypes.c_float),
                 ("rinv0", ctypes.c_float), ("rinv1", ctypes.c_float),
-                ("sigma", ctypes.c_float * FRAME_DIRS), ("reserved1", ctypes.c_int * 2),
+                ("sigma", ctypes.c_float * FRAME_DIRS), ("h0", ctypes.c_float), ("inv_h0", ctypes.c_float),
                 ("coord", ctypes.c_int * FRAME_TERMS), ("mean", ctypes.c_float * FRAME_TERMS),
                 ("dir", (ctypes.c_float * FRAME_TERMS) * FRAME_DIRS)]
 

@@ -82,7 +82,8 @@ def test_geometry_helpers():
     assert [frnn_cuda.aos_stride(d) for d in (1, 3, 4, 5, 12, 16, 17, 33, 128)] == \
         [4, 4, 4, 8, 12, 16, 32, 64, 128]
     assert frnn_cuda.aos_stride(0) == -1 and frnn_cuda.aos_stride(129) == -1
-    assert frnn_cuda.list_capacity(64) == 192 and frnn_cuda.list_capacity(0) == -1
+    assert [frnn_cuda.list_capacity(k) for k in (1, 32, 64, 65, 128)] == [160, 160, 160, 161, 224]
+    assert frnn_cuda.list_capacity(0) == -1
     assert frnn_cuda.scan_partials_count(1_000_001) == 246
 
 
@@ -135,14 +136,16 @@ def test_frame_workspace_sizes():
 
 
 def test_grid_cells():
-    # raw grids use res^g; a frame's capacity is clamp(N, 4096, 1M), at least res^g
+    # raw grids use res^g; a frame's capacity is 8 (its fine axis-0 cells per
+    # cell edge) x clamp(N, 4096, 1M), at least 8 x res^g
+    F = 8
     p = frnn_cuda.plan(100000, 3, 16, 0.1)
     assert frnn_cuda.grid_cells(100000, 3, 16, 0.1) == p["cells"]
     assert frnn_cuda.grid_cells(200000, 128, 128, 12.96) == 0
-    assert frnn_cuda.grid_cells(100000, 12, 32, 0.0345) == max(100000, frnn_cuda.plan(100000, 12, 32, 0.0345)["cells"])
-    assert frnn_cuda.grid_cells(100000, 12, 32, 0.2) == 100000
-    assert frnn_cuda.grid_cells(1000, 12, 32, 0.0345) == max(4096, frnn_cuda.plan(1000, 12, 32, 0.0345)["cells"])
-    assert frnn_cuda.grid_cells(3_000_000, 12, 32, 0.0345) == 1_000_000
+    assert frnn_cuda.grid_cells(100000, 12, 32, 0.0345) == F * max(100000, frnn_cuda.plan(100000, 12, 32, 0.0345)["cells"])
+    assert frnn_cuda.grid_cells(100000, 12, 32, 0.2) == F * 100000
+    assert frnn_cuda.grid_cells(1000, 12, 32, 0.0345) == F * max(4096, frnn_cuda.plan(1000, 12, 32, 0.0345)["cells"])
+    assert frnn_cuda.grid_cells(3_000_000, 12, 32, 0.0345) == F * 1_000_000
 
 
 @pytest.mark.skipif(gpu_visible(), reason="checks the no-device error path")

@@ -131,7 +131,7 @@ def _project(X, fi, slots):
 
 
 def _frame_build(X, K, radius):
-    """stats -> frame -> bin/count -> scan -> refine -> reorder through the seam."""
+    """stats -> frame -> bin/count -> scan -> reorder through the seam, as the engine runs them."""
     t = torch()
     N, D = X.shape
     plan = frnn_cuda._plan_struct(N, D, K, radius)
@@ -152,14 +152,12 @@ def _frame_build(X, K, radius):
     start = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
     part = t.empty(frnn_cuda.scan_partials_count(cells + 1), dtype=t.int32, device="cuda:0")
     assert L.frnn_launch_exclusive_scan(vp(cnt), cells + 1, vp(start), vp(part), None) == 0
-    assert L.frnn_launch_refine(vp(d), N, D, ctypes.byref(plan), vp(cell_of), vp(cnt), vp(rank), vp(ws),
-                                None) == 0
     ds = frnn_cuda.aos_stride(D)
     sidx = t.empty(N, dtype=t.int32, device="cuda:0")
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
     frows = t.empty(N * ds, dtype=t.float32, device="cuda:0")
-    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), None, cells,
                                  vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), None) == 0
     t.cuda.synchronize()
     out = {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start, sidx=sidx,
@@ -192,9 +190,9 @@ def _near_pairs(X, radius, nq=400, seed=5):
 @pytest.mark.parametrize("name,N", [("metric", 300_000), ("C3", 300_000)])
 def test_frame_grid_and_refinement(name, N):
     """The grid frame of first-coordinate plans: descriptor (terms, directions,
-    margin, geometry), the binning recomputed in exact fp32, the guarantee that
-    pairs within the radius fall in neighbouring cells, the sub-bin order inside
-    big cells and the reorder invariants."""
+    margin, geometry with a fine axis 0), the binning recomputed in exact fp32,
+    the guarantee that pairs within the radius fall in neighbouring cells of
+    edge h and the reorder invariants."""
     w = W.config(name, N=N)
     log(f"frame {name} N={N}")
     out = _frame_build(w.X, w.K, w.radius)
@@ -204,7 +202,7 @@ def test_frame_grid_and_refinement(name, N):
     st = out["stats"]
     mean, var, lo, hi = (st[:, k] for k in range(4))
     T = min(w.D, 32)
-    assert fi.terms == T and fi.axes == min(g + 2, T) - g
+    assert fi.terms == T and fi.axes == 0      # no refinement directions with a fine axis 0
     assert fi.bins0 * fi.bins1 == (1024 if fi.axes == 1 else 32 * 32)
     # terms: the highest-variance coordinates, lower index on ties
     coord = np.array(fi.coord[:T])
@@ -235,29 +233,37 @@ def test_frame_grid_and_refinement(name, N):
     u = 2.0 ** -24
     assert (T + 2) * u * R <= fi.margin <= 1.01 * (T + 2) * u * R
     # geometry: cell edge >= r (1 + 2^-12) + 2 margin + 2 slack, binning
-    # reciprocal rounded down, origins at -4 sigma, grid within the capacity
+    # reciprocal rounded down, origins at -4 sigma, grid within the capacity;
+    # axis 0 split into fine0 cells of edge h / fine0 (exact scalings)
     r = float(np.float32(w.radius))
     h0 = r * (1 + 2.0 ** -12) + 2 * fi.margin
     smax = max(fi.sigma[k] for k in range(g))
     assert fi.slack >= 2.0 ** -18 * (4 * smax + h0)
     assert fi.h >= h0 + 2 * fi.slack and float(fi.inv_h) * float(fi.h) <= 1.0
+    F = fi.fine0
+    assert F == 8 and np.float32(fi.h0) * F == np.float32(fi.h) and np.float32(fi.inv_h0) == np.float32(fi.inv_h) * F
     res = np.array(fi.res[:g])
+    assert res[0] % F == 0
     assert np.all(res >= 1) and fi.cells == np.prod(res) <= cap
     assert list(fi.stride[:g]) == [int(np.prod(res[:d])) for d in range(g)]
     for d in range(g):
         assert fi.lo[d] == np.float32(-4.0 * np.float64(fi.sigma[d]))
     # binning, recomputed in exact fp32
     S = _project(w.X, fi, slots)
-    cc = np.stack([_sub_bins(S[d], fi.lo[d], fi.inv_h, fi.res[d]) for d in range(g)], 1)
+    cc = np.stack([_sub_bins(S[d], fi.lo[d], fi.inv_h0 if d == 0 else fi.inv_h, fi.res[d]) for d in range(g)], 1)
     cell_of = cc @ np.array(fi.stride[:g])
     assert np.array_equal(out["cell_of"], cell_of)
     cnt = np.bincount(cell_of, minlength=cap + 1)
     assert np.array_equal(out["cnt"], cnt)
-    # the shell guarantee: pairs within the radius sit in neighbouring cells,
-    # and their projections differ by at most r (1 + 2^-15) + 2 margin
+    # the shell guarantee: pairs within the radius sit in neighbouring cells of
+    # edge h (axis 0: fine cell // fine0, the same as binning with inv_h), and
+    # their projections differ by at most r (1 + 2^-15) + 2 margin
     qq, pp = _near_pairs(w.X, w.radius)
     assert len(qq) > 1000
-    assert np.max(np.abs(cc[qq] - cc[pp])) <= 1
+    coarse = cc.copy()
+    coarse[:, 0] //= F
+    assert np.array_equal(coarse[:, 0], _sub_bins(S[0], fi.lo[0], fi.inv_h, fi.res[0] // F))
+    assert np.max(np.abs(coarse[qq] - coarse[pp])) <= 1
     for s in S:
         assert np.max(np.abs(s[pp].astype(np.float64) - s[qq])) <= r * (1 + 2.0 ** -15) + 2 * fi.margin
     # reorder invariants
@@ -272,16 +278,7 @@ def test_frame_grid_and_refinement(name, N):
     fr = out["frows"].reshape(N, ds)
     assert np.array_equal(fr[:, :w.D], (w.X[sidx] - mean[None, :]).astype(np.float32))
     assert np.all(fr[:, w.D:] == 0)
-    # sub-bin order inside cells holding >= 256 points
-    r0, r1 = S[g], S[g + 1] if fi.axes > 1 else np.zeros(N, np.float32)
-    key = _sub_bins(r0[sidx], fi.rlo0, fi.rinv0, fi.bins0) * fi.bins1
-    if fi.axes > 1:
-        key = key + _sub_bins(r1[sidx], fi.rlo1, fi.rinv1, fi.bins1)
-    big = cnt[cs] >= 256
-    same_cell = np.concatenate([[False], cs[1:] == cs[:-1]])
-    step = np.concatenate([[0], np.diff(key)])
-    assert np.all(step[same_cell & big] >= 0)
-    log(f"  res={list(res)} h/r={fi.h / r:.3f} cells={fi.cells} big-cell share={big.mean():.3f}")
+    log(f"  res={list(res)} h/r={fi.h / r:.3f} cells={fi.cells}")
 
 
 def test_frame_falls_back_to_raw_coordinates_on_infinite_input():
@@ -293,8 +290,13 @@ def test_frame_falls_back_to_raw_coordinates_on_infinite_input():
     out = _frame_build(X, 16, 0.1)
     fi, plan = out["frame"], out["plan"]
     assert plan.path == 2 and fi.projected == 0 and fi.axes == 0
-    assert fi.cells == plan.cells and list(fi.res[:plan.grid_dim]) == [plan.res] * plan.grid_dim
-    want = O.bin_cells(X, plan.grid_dim, plan.res, np.float32(plan.inv_cell))
+    g, F = plan.grid_dim, fi.fine0
+    assert fi.cells == F * plan.cells and list(fi.res[:g]) == [F * plan.res] + [plan.res] * (g - 1)
+    # the plan's cells, axis 0 split F ways: fine x, then the reference's hash
+    # of the other coordinates
+    fine_x = np.clip(np.floor(X[:, 0] * np.float32(plan.inv_cell * F)), 0, F * plan.res - 1).astype(np.int64)
+    ref = O.bin_cells(X, g, plan.res, np.float32(plan.inv_cell))
+    want = fine_x + F * plan.res * (ref // plan.res)
     assert np.array_equal(out["cell_of"], want)
 
 
@@ -349,15 +351,12 @@ def test_seam_search_first_coordinate_plan(framed):
     start = t.empty(cells + 1, dtype=t.int32, device="cuda:0")
     part = t.empty(frnn_cuda.scan_partials_count(cells + 1), dtype=t.int32, device="cuda:0")
     assert L.frnn_launch_exclusive_scan(vp(cnt), cells + 1, vp(start), vp(part), None) == 0
-    if framed:
-        assert L.frnn_launch_refine(vp(d), N, D, ctypes.byref(plan), vp(cell_of), vp(cnt), vp(rank), vp(ws),
-                                    None) == 0
     ds = frnn_cuda.aos_stride(D)
     sidx = t.empty(N, dtype=t.int32, device="cuda:0")
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
     assert L.frnn_uses_filter_rows(D) == 0
-    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), vp(ws), cells,
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), None, cells,
                                  vp(sidx), vp(inv_p), vp(aos), None, None, None) == 0
     cap = frnn_cuda.list_capacity(K)
     lists = t.empty(N * cap, dtype=t.int64, device="cuda:0")

@@ -196,7 +196,7 @@ def test_profiling_counters_and_stage_times():
     assert eng.last_plan()["path"] == "grid_first"
     st = eng.stage_times()
     c = eng.counters()
-    assert st["frame"] > 0 and st["refine"] > 0
+    assert st["frame"] > 0
     assert c["shell_candidates"] >= c["accepted"]
     assert c["streamed_pairs"] >= c["filter_hits"] >= c["accepted"] > 0
     eng.close()
