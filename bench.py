@@ -58,12 +58,8 @@ def build_bytes(N, D, ds, g, C, framed):
     }
     if framed:
         # frame: covariance sample over the T projection terms (512 tiles of 256
-        # points); refine: big-cell flags scan + the sub-bin pass's reads of
-        # every point's cell and count; the reorder also reads the keys
+        # points)
         b["frame"] = 4 * T * min(N, 512 * 256)
-        # (the sub-bin work of big-cell points is data dependent and not counted)
-        b["refine"] = 8 * (C + 1) + 8 * N
-        b["reorder"] += 4 * N
     return b
 
 

@@ -74,39 +74,36 @@ typedef struct frnn_dim_stat {
  * grids the data along its own principal directions instead of the first g
  * coordinates, which shrinks the shells of low-rank data several-fold.
  *
- * Projection of point x onto direction k (0 <= k < 6):
+ * Projection of point x onto direction k (0 <= k < grid_dim):
  *   s = 0;  s = fmaf(dir[k][t], fl(x[coord[t]] - mean[t]), s)  for t = 0..terms-1
  * (sequential fp32 fma chain; the weights of each direction have norm < 1 and the
- * grid directions are orthonormal up to a 2^-18 shrink); margin bounds |computed -
- * exact projection| over every finite input point.  Directions 0..grid_dim-1 are
- * the grid axes: cell coordinate c_k = clamp(floor((s_k - lo[k]) * inv_h), 0,
- * res[k] - 1) (inv_h0 for k = 0) and cell id sum_k c_k * stride[k].  Directions 4 and 5 order the
- * points inside cells of >= 256 points: sub-bin clamp(floor((s - rlo) * rinv),
- * 0, bins - 1).  projected == 0 (infinite input) falls back to the first
- * grid_dim raw coordinates with the plan's cell size and resolution. */
+ * directions are orthonormal up to a 2^-18 shrink); margin bounds |computed -
+ * exact projection| over every finite input point.  Cell coordinate
+ * c_k = clamp(floor((s_k - lo[k]) * inv_h), 0, res[k] - 1) (inv_h0 for k = 0)
+ * and cell id sum_k c_k * stride[k].  Direction 0 has fine0 cells per cell edge
+ * h, so the points of a row of cells (fixed c_1..c_{g-1}) are ordered by their
+ * projection on it.  projected == 0 (infinite input) falls back to the first
+ * grid_dim raw coordinates with the plan's cell size and resolution (axis 0
+ * still split fine0 ways). */
 #define FRNN_FRAME_TERMS 32
-#define FRNN_FRAME_DIRS 6
+#define FRNN_FRAME_DIRS 4
 typedef struct frnn_frame {
     int grid_dim;          /* gridded directions g */
     int cells;             /* prod res[k] */
     int terms;             /* coordinates per projection, <= FRNN_FRAME_TERMS */
-    int axes;              /* refinement directions (0, 1 or 2) */
     int projected;         /* 1: principal directions; 0: raw first coordinates */
-    int bins0, bins1;      /* refinement sub-bins per direction; bins0 * bins1 == 1024 */
     int fine0;             /* cells of direction 0 per cell edge h (its cells are h / fine0 wide) */
-    int res[4];            /* cells per grid direction */
-    int stride[4];         /* cell-id stride per grid direction, stride[0] == 1 */
-    float lo[4];           /* grid origin per direction */
+    int res[FRNN_FRAME_DIRS];      /* cells per grid direction */
+    int stride[FRNN_FRAME_DIRS];   /* cell-id stride per grid direction, stride[0] == 1 */
+    float lo[FRNN_FRAME_DIRS];     /* grid origin per direction */
     float h, inv_h;        /* cell edge and fl(1/h) */
     float margin;          /* projection rounding bound */
     float slack;           /* binning rounding bound on a cell boundary */
-    float rlo0, rlo1;      /* refinement bin origin per direction */
-    float rinv0, rinv1;    /* refinement bins per unit (0: a single bin) */
-    float sigma[6];        /* standard deviation of the projections per direction */
     float h0, inv_h0;      /* direction 0's cell edge h / fine0 and fl(1/h0) */
+    float sigma[FRNN_FRAME_DIRS];  /* standard deviation of the projections per direction */
     int coord[FRNN_FRAME_TERMS];               /* term coordinates, highest variance first */
     float mean[FRNN_FRAME_TERMS];              /* term centres (the point-statistics means) */
-    float dir[FRNN_FRAME_DIRS][FRNN_FRAME_TERMS];   /* 0..3 grid, 4..5 refinement */
+    float dir[FRNN_FRAME_DIRS][FRNN_FRAME_TERMS];   /* grid directions */
 } frnn_frame_t;
 
 /* ---- host-only helpers (no HIP call) ------------------------------------ */
@@ -165,9 +162,8 @@ int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
  * events; FRNN_PROFILE_COUNTERS runs the counting build of the search kernel
  * and reads its work counters back after each search (0: neither).  Stages:
  * 0 zero-fill, 1 point statistics, 2 grid frame, 3 bin+count, 4 scan,
- * 5 within-cell refinement, 6 reorder/transpose, 7 neighbour search,
- * 8 unpermute. */
-#define FRNN_NUM_STAGES 9
+ * 5 reorder/transpose, 6 neighbour search, 7 unpermute. */
+#define FRNN_NUM_STAGES 8
 #define FRNN_PROFILE_EVENTS 1
 #define FRNN_PROFILE_COUNTERS 2
 int frnn_engine_set_profiling(frnn_engine_t* engine, int flags);
@@ -187,8 +183,8 @@ int frnn_engine_counters(const frnn_engine_t* engine, long long* out, int n);
 
 /* Cell count a plan's grid uses: res^g, except for first-coordinate plans with
  * dim > grid_dim (which have a frame): the frame's capacity
- * max(min(max(N, 4096), FRNN_MAX_CELLS), res^g) (the frame picks its
- * resolution to fit).
+ * fine0 * max(min(max(N, 4096), FRNN_MAX_CELLS), res^g) with fine0 = 8 (the
+ * frame picks its resolution to fit), at most 8 * FRNN_MAX_CELLS.
  * Count arrays hold cells + 1 ints. */
 long long frnn_grid_cells(int N, int dim, const frnn_plan_t* plan);
 
@@ -211,32 +207,23 @@ int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partia
 long long frnn_stats_workspace_bytes(int dim);
 int frnn_launch_point_stats(const float* d_points_soa, int N, int dim, void* d_stats_ws, void* stream);
 
-/* Grid frame and within-cell refinement of first-coordinate plans (no
- * reference counterpart; frnn_frame_t).  frnn_frame_workspace_bytes() bytes at
- * d_frame_ws (0: the plan has no frame).  frnn_launch_frame writes the frame
- * (principal directions of the up to 32 highest-variance coordinates from a
- * sampled covariance; needs the point statistics); run it before binning.
- * frnn_launch_refine (after the scan) gives cells holding >= 256 points 1024
- * sub-bins on the refinement directions and replaces d_rank of their points by
- * the sub-bin arrival slot: the reference's within-cell order is atomic arrival
- * order (insert_points.cu:156-158), so any order is admissible. */
+/* Grid frame of first-coordinate plans (no reference counterpart;
+ * frnn_frame_t).  frnn_frame_workspace_bytes() bytes at d_frame_ws (0: the plan
+ * has no frame).  frnn_launch_frame writes the frame (principal directions of
+ * the up to 32 highest-variance coordinates from a sampled covariance; needs
+ * the point statistics); run it before binning. */
 long long frnn_frame_workspace_bytes(int N, int dim, const frnn_plan_t* plan);
 int frnn_launch_frame(const float* d_points_soa, int N, int dim, const frnn_plan_t* plan,
                       const void* d_stats_ws, void* d_frame_ws, void* stream);
-int frnn_launch_refine(const float* d_points_soa, int N, int dim, const frnn_plan_t* plan,
-                       const int* d_cell_of, const int* d_cnt, int* d_rank, void* d_frame_ws,
-                       void* stream);
 
 /* run_counting_sort / run_counting_sort_aos3 (insert_points.cu:142-164,205-226):
- * pos = d_start[cell] + rank (+ the sub-bin offset inside refined cells);
- * d_sorted_idx[pos] = i; d_inv[i] = pos; AoS row pos of d_sorted_aos (stride
- * frnn_aos_stride(dim), zero padded) = point i.  With d_frows (needs
- * d_stats_ws), row pos of d_frows also gets the centred row fl(x - mean), which
- * the search streams when frnn_uses_filter_rows(dim).  d_frame_ws, d_stats_ws
- * and d_frows may be NULL; cells as frnn_grid_cells. */
+ * pos = d_start[cell] + rank; d_sorted_idx[pos] = i; d_inv[i] = pos; AoS row
+ * pos of d_sorted_aos (stride frnn_aos_stride(dim), zero padded) = point i.
+ * With d_frows (needs d_stats_ws), row pos of d_frows also gets the centred
+ * row fl(x - mean), which the search streams when frnn_uses_filter_rows(dim).
+ * d_stats_ws and d_frows may be NULL. */
 int frnn_launch_reorder(const float* d_points_soa, int N, int dim, const int* d_cell_of,
-                        const int* d_rank, const int* d_start, const int* d_cnt,
-                        const void* d_frame_ws, long long cells, int* d_sorted_idx, int* d_inv,
+                        const int* d_rank, const int* d_start, int* d_sorted_idx, int* d_inv,
                         float* d_sorted_aos, const void* d_stats_ws, float* d_frows, void* stream);
 
 /* Brute-force input staging: AoS copy of the SoA points in original order,

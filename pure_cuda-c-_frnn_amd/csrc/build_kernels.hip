@@ -63,20 +63,17 @@ __device__ __forceinline__ int block_exclusive_scan_256(int v, int* s_tmp, int* 
     return incl - v;
 }
 
-// flag_min > 0: the scanned value is (in[i] >= flag_min), e.g. "cell is big".
-__device__ __forceinline__ int scan_value(const int* __restrict__ in, long long idx, int n, int flag_min) {
-    if (idx >= n) return 0;
-    const int v = in[idx];
-    return flag_min > 0 ? (v >= flag_min ? 1 : 0) : v;
+__device__ __forceinline__ int scan_value(const int* __restrict__ in, long long idx, int n) {
+    return idx < n ? in[idx] : 0;
 }
 
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int* __restrict__ in, int n,
-                                                                   int* __restrict__ partials, int flag_min) {
+                                                                   int* __restrict__ partials) {
     __shared__ int s_tmp[kScanThreads];
     const long long base = (long long)blockIdx.x * kScanTile + (long long)threadIdx.x * kScanItems;
     int sum = 0;
 #pragma unroll
-    for (int j = 0; j < kScanItems; ++j) sum += scan_value(in, base + j, n, flag_min);
+    for (int j = 0; j < kScanItems; ++j) sum += scan_value(in, base + j, n);
     int total;
     block_exclusive_scan_256(sum, s_tmp, &total);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
@@ -104,14 +101,14 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int* __rest
 
 __global__ __launch_bounds__(kScanThreads) void scan_final_kernel(const int* __restrict__ in, int n,
                                                                   const int* __restrict__ partials,
-                                                                  int* __restrict__ out, int flag_min) {
+                                                                  int* __restrict__ out) {
     __shared__ int s_tmp[kScanThreads];
     const long long base = (long long)blockIdx.x * kScanTile + (long long)threadIdx.x * kScanItems;
     int v[kScanItems];
     int sum = 0;
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) {
-        v[j] = scan_value(in, base + j, n, flag_min);
+        v[j] = scan_value(in, base + j, n);
         sum += v[j];
     }
     int total;
@@ -150,17 +147,11 @@ __device__ __forceinline__ void write_row(const float* __restrict__ pts, int N, 
 }
 
 // One thread per point: SoA reads are coalesced per axis; the AoS row store
-// is ds/4 16-byte vector stores to one contiguous row.  Points of big cells go
-// to their sub-bin's range of the cell (within-cell refinement order, sub-bin
-// key from sub_count_kernel).
+// is ds/4 16-byte vector stores to one contiguous row.
 __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ pts, int N, int D, int ds,
                                                       const int* __restrict__ cell_of,
                                                       const int* __restrict__ rank,
                                                       const int* __restrict__ start,
-                                                      const int* __restrict__ cnt,
-                                                      const int* __restrict__ subkey,
-                                                      const int* __restrict__ bidx,
-                                                      const int* __restrict__ substart,
                                                       int* __restrict__ sorted_idx,
                                                       int* __restrict__ inv,
                                                       float* __restrict__ aos,
@@ -168,11 +159,7 @@ __global__ __launch_bounds__(256) void reorder_kernel(const float* __restrict__ 
                                                       float* __restrict__ frows) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= N) return;
-    const int c = cell_of[i];
-    int pos = start[c] + rank[i];
-    if (subkey && cnt[c] >= kBigCell) {
-        pos += substart[(size_t)bidx[c] * kSubStride + subkey[i]];
-    }
+    const int pos = start[cell_of[i]] + rank[i];
     sorted_idx[pos] = i;
     inv[i] = pos;
     write_row(pts, N, D, ds, i, pos, aos, st, frows);
@@ -275,7 +262,7 @@ __global__ __launch_bounds__(128) void stats_setup_kernel(const float* __restric
 // non-finite bound (infinite input) is stored as +inf; frame_dirs_kernel then
 // falls back to the raw first coordinates.
 __global__ __launch_bounds__(128) void frame_terms_kernel(const DimStat* __restrict__ st, int g, int D,
-                                                          int fine0, Frame* __restrict__ f) {
+                                                          Frame* __restrict__ f) {
     __shared__ float s_var[FRNN_MAX_DIM];
     __shared__ int s_coord[kMaxTerms];
     const int tid = threadIdx.x;
@@ -312,12 +299,6 @@ __global__ __launch_bounds__(128) void frame_terms_kernel(const DimStat* __restr
     }
     f->g = g;
     f->terms = T;
-    // grid + refinement directions (none with a fine axis 0, which orders
-    // the points inside cells instead)
-    const int m = (g + 2 < T && fine0 == 1) ? g + 2 : (g < T ? g : T);
-    f->L = m > g ? m - g : 0;
-    f->nb1 = f->L == 2 ? 32 : kSubBins;
-    f->nb2 = f->L == 2 ? 32 : 1;
     const double E = (T + 2) * 5.9604644775390625e-08 * sqrt(R2) * (1.0 + 9.765625e-04);
     f->margin = E < 1.0e30 ? (float)(E * (1.0 + 9.5367431640625e-07)) : __builtin_huge_valf();
     f->projected = 1;
@@ -432,12 +413,11 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 
 // Principal directions and geometry of a frame (fp64, one wave; lane t holds
-// component t of every direction).  The m = g + L leading eigenvectors of the
-// sampled covariance C come from orthogonal iteration on (C / cmax)^8 (three
+// component t of every direction).  The g leading eigenvectors of the sampled
+// covariance C come from orthogonal iteration on (C / cmax)^8 (three
 // squarings in LDS, then 2 steps: 16 steps' worth on C; modified
 // Gram-Schmidt); each direction's variance is its Rayleigh quotient on C.
-// Directions 0..g-1 become the grid axes, the next L the refinement
-// directions (slots 4, 5); weights are scaled by 1 - 2^-18, so the fp32 grid
+// They become the grid axes; weights are scaled by 1 - 2^-18, so the fp32
 // directions stay orthonormal up to a shrink (|U d| <= |d| for any d) and
 // every direction has norm < 1.
 //
@@ -447,9 +427,9 @@ constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 // distance < r2, so |p - q| <= r (1 + 2^-15)) have computed projections closer
 // than r (1 + 2^-15) + 2 margin; with the rounding of the binning (bounded by
 // slack) their cell coordinates differ by at most one, so every neighbour lies
-// in the query's 3^g shell.  Refinement sub-bins span +-2.5 sigma.  An
-// infinite margin falls back to the raw first g coordinates with the plan's
-// cell size.
+// in the query's 3^g shell of cells of edge h (axis 0: fine0 cells of edge
+// h / fine0 each).  An infinite margin falls back to the raw first g
+// coordinates with the plan's cell size.
 __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict__ covsum, double nsamp,
                                                         float radius, float cell_raw, float inv_cell_raw,
                                                         int res_raw, int cells_cap, int fine0,
@@ -461,7 +441,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     const int t = threadIdx.x;
     const int T = f->terms;
     const int g = f->g;
-    const int m = g + f->L;
+    const int m = g;
     const int P = T * (T + 1) / 2;
     for (int i = t; i < kMaxTerms * (kMaxTerms + 1); i += kWave) {
         (&s_C[0][0])[i] = 0.0;
@@ -575,8 +555,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     }
     // Orthogonal iteration leaves direction j converged towards eigenvector j
     // (descending eigenvalues); its variance is the Rayleigh quotient v_j' C v_j.
-    // A rotation inside the subspace would not change the captured variance,
-    // and the order only steers which directions grid and which refine.
+    // A rotation inside the subspace would not change the captured variance.
     double lam[kMaxDirs];
     {
         double w[kMaxDirs];
@@ -588,19 +567,17 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
 #pragma unroll
     for (int j = 0; j < kMaxDirs; ++j) {
         if (j >= m) break;
-        const int slot = j < g ? j : kRefDir0 + (j - g);
-        if (on) f->dir[slot][t] = (float)(v[j] * kShrink);
-        if (t == 0) f->sigma[slot] = (float)sqrt(fmax(lam[j], 0.0));
+        if (on) f->dir[j][t] = (float)(v[j] * kShrink);
+        if (t == 0) f->sigma[j] = (float)sqrt(fmax(lam[j], 0.0));
     }
     if (t != 0) return;
     // ---- geometry (one thread) ----
     const bool exact = f->margin < 1.0e30f;
     f->fine0 = fine0;
     if (!exact) {
-        // infinite input: grid on the raw first g coordinates, no refinement
-        // (axis 0 still in fine0 cells per plan cell)
+        // infinite input: grid on the raw first g coordinates (axis 0 still
+        // in fine0 cells per plan cell)
         f->projected = 0;
-        f->L = 0;
         f->margin = 0.0f;
         f->slack = 0.0f;
         f->h = cell_raw;
@@ -615,7 +592,6 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
             stride *= f->res[d];
         }
         f->cells = stride;
-        f->rlo0 = f->rlo1 = f->rinv0 = f->rinv1 = 0.0f;
         return;
     }
     double sig[kFrameGrid];
@@ -669,21 +645,6 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
         stride *= res[d];
     }
     f->cells = stride;
-    // refinement sub-bins over +-2.5 sigma of each refinement direction
-    float rlo[2] = {0.0f, 0.0f}, rinv[2] = {0.0f, 0.0f};
-    const int nb[2] = {f->nb1, f->nb2};
-    for (int k = 0; k < f->L; ++k) {
-        const double sg = (double)f->sigma[kRefDir0 + k];
-        const double iv = (double)nb[k] / (5.0 * sg);
-        if (sg > 0.0 && iv < 1.0e30) {
-            rlo[k] = (float)(-2.5 * sg);
-            rinv[k] = (float)iv;
-        }
-    }
-    f->rlo0 = rlo[0];
-    f->rlo1 = rlo[1];
-    f->rinv0 = rinv[0];
-    f->rinv1 = rinv[1];
 }
 
 // Binning on a frame's grid directions: projections (or, without a
@@ -698,7 +659,7 @@ __global__ __launch_bounds__(256) void bin_frame_kernel(const float* __restrict_
     const int g = f->g;
     float s[kFrameGrid];
     if (f->projected) {
-        frame_project(f, 0, [&](int d) { return pts[(size_t)d * N + i]; }, s);
+        frame_project(f, [&](int d) { return pts[(size_t)d * N + i]; }, s);
     } else {
 #pragma unroll
         for (int d = 0; d < kFrameGrid; ++d) s[d] = d < g ? pts[(size_t)d * N + i] : 0.0f;
@@ -710,72 +671,6 @@ __global__ __launch_bounds__(256) void bin_frame_kernel(const float* __restrict_
     c = c < cells ? c : cells - 1;   // the frame fits `cells`; a mismatched count array stays in bounds
     cell_of[i] = c;
     rank[i] = atomicAdd(&cnt[c], 1);
-}
-
-// Sub-bin key and counting inside big cells; the arrival slot in the sub-bin
-// replaces the cell rank, and the key is kept for the reorder.
-__global__ __launch_bounds__(256) void sub_count_kernel(const float* __restrict__ pts, int N,
-                                                        const int* __restrict__ cell_of,
-                                                        const int* __restrict__ cnt,
-                                                        const int* __restrict__ bidx,
-                                                        const Frame* __restrict__ f,
-                                                        int* __restrict__ subcnt, int* __restrict__ rank,
-                                                        int* __restrict__ subkey) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= N) return;
-    const int c = cell_of[i];
-    if (cnt[c] < kBigCell) return;
-    float s[2];
-    frame_project(f, kRefDir0, [&](int d) { return pts[(size_t)d * N + i]; }, s);
-    const int q1 = sub_bin(s[0], f->rlo0, f->rinv0, f->nb1);
-    const int q2 = f->L > 1 ? sub_bin(s[1], f->rlo1, f->rinv1, f->nb2) : 0;
-    const int key = q1 * f->nb2 + q2;
-    subkey[i] = key;
-    rank[i] = atomicAdd(&subcnt[(size_t)bidx[c] * kSubBins + key], 1);
-}
-
-// Sub-bin tables of the big cells: block b (one per possible big cell) clears
-// (zero_sub_kernel) or exclusively scans (sub_scan_kernel, 1025 entries, the
-// last the cell's total) the 1024 sub-bin counts of big cell b; blocks past
-// the number of big cells (bidx[cells]) exit at once.
-__global__ __launch_bounds__(256) void zero_sub_kernel(const int* __restrict__ bidx, long long cells,
-                                                       int* __restrict__ subcnt) {
-    if ((int)blockIdx.x >= bidx[cells]) return;
-    int* row = subcnt + (size_t)blockIdx.x * kSubBins;
-    for (int k = threadIdx.x; k < kSubBins; k += blockDim.x) row[k] = 0;
-}
-
-__global__ __launch_bounds__(256) void sub_scan_kernel(const int* __restrict__ bidx, long long cells,
-                                                       const int* __restrict__ subcnt,
-                                                       int* __restrict__ substart) {
-    constexpr int kPer = kSubBins / 256;
-    __shared__ int s_part[256];
-    if ((int)blockIdx.x >= bidx[cells]) return;
-    const int tid = threadIdx.x;
-    const int* row = subcnt + (size_t)blockIdx.x * kSubBins;
-    int v[kPer];
-    int sum = 0;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        v[j] = row[tid * kPer + j];
-        sum += v[j];
-    }
-    s_part[tid] = sum;
-    __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {   // inclusive scan of the per-thread sums
-        const int y = tid >= o ? s_part[tid - o] : 0;
-        __syncthreads();
-        s_part[tid] += y;
-        __syncthreads();
-    }
-    int run = s_part[tid] - sum;
-    int* out = substart + (size_t)blockIdx.x * kSubStride;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        out[tid * kPer + j] = run;
-        run += v[j];
-    }
-    if (tid == 255) out[kSubBins] = run;
 }
 
 __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ pts, int N, int D, int ds,
@@ -876,33 +771,25 @@ int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, co
 
 int scan_partials_count(int n) { return (n + kScanTile - 1) / kScanTile + 1; }
 
-int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s, int flag_min) {
+int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s) {
     if (n <= 0) return 0;
     const int nb = (n + kScanTile - 1) / kScanTile;
     if (nb > kScanTile) return 2;
-    hipLaunchKernelGGL(scan_reduce_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, flag_min);
+    hipLaunchKernelGGL(scan_reduce_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials);
     hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partials, nb);
-    hipLaunchKernelGGL(scan_final_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out, flag_min);
+    hipLaunchKernelGGL(scan_final_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out);
     return launch_result();
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-FrameLayout frame_layout(int N, int D, long long cells) {
+FrameLayout frame_layout() {
     FrameLayout L{};
-    L.max_big = N / kBigCell;
     size_t off = 0;
     L.frame = off;    off = align256(off + sizeof(Frame));
-    L.bidx = off;     off = align256(off + (size_t)(cells + 1) * sizeof(int));
-    L.subcnt = off;   off = align256(off + (size_t)L.max_big * kSubBins * sizeof(int));
-    L.substart = off; off = align256(off + (size_t)L.max_big * kSubStride * sizeof(int));
-    const int np = scan_partials_count((int)(cells + 1));
-    L.scanpart = off; off = align256(off + (size_t)np * sizeof(int));
     L.cov = off;      off = align256(off + (size_t)kCovBlocks * kMaxPairs * sizeof(double));
     L.covsum = off;   off = align256(off + (size_t)kMaxPairs * sizeof(double));
-    L.subkey = off;   off = align256(off + (size_t)N * sizeof(int));
     L.total = off;
-    (void)D;
     return L;
 }
 
@@ -928,12 +815,12 @@ int launch_point_stats(const float* pts, int N, int D, void* stats_ws, hipStream
 int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long long cells,
                  const void* stats_ws, void* ws, hipStream_t s) {
     if (N <= 0 || !has_frame(plan, D)) return 0;
-    const FrameLayout L = frame_layout(N, D, cells);
+    const FrameLayout L = frame_layout();
     char* base = static_cast<char*>(ws);
     Frame* f = reinterpret_cast<Frame*>(base + L.frame);
     const DimStat* st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
     double* cov = reinterpret_cast<double*>(base + L.cov);
-    hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(128), 0, s, st, plan.grid_dim, D, kFine0, f);
+    hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(128), 0, s, st, plan.grid_dim, D, f);
     // covariance sample: kCovBlocks tiles of 256 consecutive points, evenly spaced
     const long long tile_stride = N <= (long long)kCovBlocks * 256 ? 256 : (long long)N / kCovBlocks;
     long long nsamp = 0;
@@ -949,50 +836,17 @@ int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long l
     return launch_result();
 }
 
-int launch_refine(const float* pts, int N, int D, long long cells, const int* cell_of, const int* cnt,
-                  int* rank, void* ws, hipStream_t s) {
-    if (N <= 0) return 0;
-    const FrameLayout L = frame_layout(N, D, cells);
-    char* base = static_cast<char*>(ws);
-    const Frame* f = reinterpret_cast<const Frame*>(base + L.frame);
-    int* bidx = reinterpret_cast<int*>(base + L.bidx);
-    int* subcnt = reinterpret_cast<int*>(base + L.subcnt);
-    int* substart = reinterpret_cast<int*>(base + L.substart);
-    int* scanpart = reinterpret_cast<int*>(base + L.scanpart);
-    int* subkey = reinterpret_cast<int*>(base + L.subkey);
-    const int rc = launch_exclusive_scan(cnt, (int)cells + 1, bidx, scanpart, s, kBigCell);
-    if (rc) return rc;
-    if (L.max_big == 0) return launch_result();   // no cell can hold kBigCell points
-    hipLaunchKernelGGL(zero_sub_kernel, dim3(L.max_big), dim3(256), 0, s, bidx, cells, subcnt);
-    hipLaunchKernelGGL(sub_count_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, cell_of, cnt,
-                       bidx, f, subcnt, rank, subkey);
-    hipLaunchKernelGGL(sub_scan_kernel, dim3(L.max_big), dim3(256), 0, s, bidx, cells, subcnt, substart);
-    return launch_result();
-}
-
 static const DimStat* stats_of(const void* stats_ws, int D) {
     return stats_ws ? reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims)
                     : nullptr;
 }
 
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,
-                   const int* cnt, const void* frame_ws, long long cells, int* sorted_idx, int* inv,
-                   float* aos, const void* stats_ws, float* frows, hipStream_t s) {
+                   int* sorted_idx, int* inv, float* aos, const void* stats_ws, float* frows, hipStream_t s) {
     if (N <= 0) return 0;
     if (frows && !stats_ws) return 1;
-    const int* subkey = nullptr;
-    const int* bidx = nullptr;
-    const int* substart = nullptr;
-    if (frame_ws) {
-        const FrameLayout L = frame_layout(N, D, cells);
-        const char* base = static_cast<const char*>(frame_ws);
-        subkey = reinterpret_cast<const int*>(base + L.subkey);
-        bidx = reinterpret_cast<const int*>(base + L.bidx);
-        substart = reinterpret_cast<const int*>(base + L.substart);
-    }
     hipLaunchKernelGGL(reorder_kernel, dim3(blocks_for(N, 256)), dim3(256), 0, s, pts, N, D,
-                       aos_stride(D), cell_of, rank, start, cnt, subkey, bidx, substart, sorted_idx, inv, aos,
-                       stats_of(stats_ws, D), frows);
+                       aos_stride(D), cell_of, rank, start, sorted_idx, inv, aos, stats_of(stats_ws, D), frows);
     return launch_result();
 }
 

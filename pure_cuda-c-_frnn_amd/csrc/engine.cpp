@@ -99,7 +99,7 @@ struct frnn_engine {
     float* out_dist = nullptr;
     float* aos = nullptr;
     size_t aos_bytes = 0;
-    void* frame_ws = nullptr;     // grid frame and within-cell refinement tables
+    void* frame_ws = nullptr;     // grid frame and its covariance scratch
     size_t frame_bytes = 0;
     void* stats_ws = nullptr;     // per-coordinate statistics (filter centre, frame terms)
     float* frows = nullptr;       // centred filter rows (wide rows only), stride aos_stride(dim)
@@ -163,7 +163,7 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     const long long cells = grid ? frnn::grid_cells(N, dim, plan) : 0;
     const void* frame = nullptr;
     if (framed) {
-        ST_TRY(grow((char**)&e->frame_ws, &e->frame_bytes, frnn::frame_layout(N, dim, cells).total,
+        ST_TRY(grow((char**)&e->frame_ws, &e->frame_bytes, frnn::frame_layout().total,
                     "allocating the grid frame"));
         frame = e->frame_ws;
     }
@@ -197,38 +197,28 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
         ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)cells + 1, e->start, e->partials, s),
                              "scan launch"));
     ST_TRY(mark(5));
-    // stage 5: within-cell refinement of big cells: none (a frame orders the
-    // points of a cell by its fine axis 0 instead)
-    const bool refined = framed && frnn::kFine0 == 1;
-    if (refined)
-        ST_TRY(launch_status(frnn::launch_refine(d_pts, N, dim, cells, e->cell_of, e->cnt, e->rank,
-                                                 e->frame_ws, s),
-                             "refinement launch"));
-    ST_TRY(mark(6));
-    // stage 6: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
+    // stage 5: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
     // brute force, the AoS copy
     if (grid)
-        ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start, e->cnt,
-                                                  refined ? frame : nullptr, cells, e->sorted_idx, e->inv,
-                                                  e->aos, e->stats_ws,
-                                                  frows, s),
+        ST_TRY(launch_status(frnn::launch_reorder(d_pts, N, dim, e->cell_of, e->rank, e->start, e->sorted_idx,
+                                                  e->inv, e->aos, e->stats_ws, frows, s),
                              "reorder launch"));
     else
         ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, e->stats_ws, frows, s),
                              "transpose launch"));
-    ST_TRY(mark(7));
-    // stage 7: neighbour search
+    ST_TRY(mark(6));
+    // stage 6: neighbour search
     ST_TRY(launch_status(frnn::launch_search(e->aos, frows, e->stats_ws, grid ? e->sorted_idx : nullptr,
                                              grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
                                              N, dim, K, plan, e->lists, cap,
                                              e->counting ? e->counters : nullptr, s),
                          "search launch"));
-    ST_TRY(mark(8));
-    // stage 8: results to the original query order (ScatterToOrigKernel)
+    ST_TRY(mark(7));
+    // stage 7: results to the original query order (ScatterToOrigKernel)
     ST_TRY(launch_status(frnn::launch_unpermute(e->lists, cap, grid ? e->inv : nullptr, N, K,
                                                 e->out_idx, e->out_dist, s),
                          "unpermute launch"));
-    ST_TRY(mark(9));
+    ST_TRY(mark(8));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
     if (e->profiling)
         for (int i = 0; i < FRNN_NUM_STAGES; ++i)
@@ -527,7 +517,7 @@ int frnn_launch_point_stats(const float* d_pts, int N, int dim, void* d_stats_ws
 long long frnn_frame_workspace_bytes(int N, int dim, const frnn_plan_t* plan) {
     if (!plan || N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return -1;
     if (N == 0 || !frnn::has_frame(*plan, dim)) return 0;
-    return (long long)frnn::frame_layout(N, dim, frnn::grid_cells(N, dim, *plan)).total;
+    return (long long)frnn::frame_layout().total;
 }
 
 static int check_frame_plan(int N, int dim, const frnn_plan_t* plan) {
@@ -549,35 +539,20 @@ int frnn_launch_frame(const float* d_pts, int N, int dim, const frnn_plan_t* pla
                          "frame launch");
 }
 
-int frnn_launch_refine(const float* d_pts, int N, int dim, const frnn_plan_t* plan, const int* d_cell_of,
-                       const int* d_cnt, int* d_rank, void* d_frame_ws, void* stream) {
-    ST_TRY(check_frame_plan(N, dim, plan));
-    if (N == 0) return FRNN_OK;
-    if (!d_pts || !d_cell_of || !d_cnt || !d_rank || !d_frame_ws)
-        return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    return launch_status(frnn::launch_refine(d_pts, N, dim, frnn::grid_cells(N, dim, *plan), d_cell_of, d_cnt,
-                                             d_rank, d_frame_ws, (hipStream_t)stream),
-                         "refinement launch");
-}
-
 int frnn_uses_filter_rows(int dim) {
     if (dim < 1 || dim > FRNN_MAX_DIM) return -1;
     return frnn::uses_filter_rows(dim) ? 1 : 0;
 }
 
 int frnn_launch_reorder(const float* d_pts, int N, int dim, const int* d_cell_of, const int* d_rank,
-                        const int* d_start, const int* d_cnt, const void* d_frame_ws, long long cells,
-                        int* d_sorted_idx, int* d_inv, float* d_sorted_aos, const void* d_stats_ws,
-                        float* d_frows, void* stream) {
+                        const int* d_start, int* d_sorted_idx, int* d_inv, float* d_sorted_aos,
+                        const void* d_stats_ws, float* d_frows, void* stream) {
     if (N < 0 || dim < 1 || dim > FRNN_MAX_DIM) return fail(FRNN_ERR_INVALID_ARGUMENT, "bad N or dim");
     if (N > 0 && (!d_pts || !d_cell_of || !d_rank || !d_start || !d_sorted_idx || !d_inv || !d_sorted_aos))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    if (d_frame_ws && (!d_cnt || cells < 1 || cells > (long long)frnn::kFine0 * FRNN_MAX_CELLS))
-        return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame needs the counts and the cell count");
     if (d_frows && !d_stats_ws) return fail(FRNN_ERR_INVALID_ARGUMENT, "filter rows need the statistics");
-    return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_cnt, d_frame_ws,
-                                              cells, d_sorted_idx, d_inv, d_sorted_aos, d_stats_ws, d_frows,
-                                              (hipStream_t)stream),
+    return launch_status(frnn::launch_reorder(d_pts, N, dim, d_cell_of, d_rank, d_start, d_sorted_idx, d_inv,
+                                              d_sorted_aos, d_stats_ws, d_frows, (hipStream_t)stream),
                          "reorder launch");
 }
 

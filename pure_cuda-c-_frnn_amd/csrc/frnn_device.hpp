@@ -25,8 +25,8 @@ __device__ __forceinline__ int bin_coord(float x, float inv_cell, int res) {
     return (int)f;
 }
 
-// Sub-bin of a refinement axis: floor((x - lo) * inv) clamped to [0, nb-1].
-// Monotone in x, so an interval of x maps onto an interval of sub-bins.
+// Cell of a frame axis: floor((x - lo) * inv) clamped to [0, nb-1].
+// Monotone in x, so an interval of x maps onto an interval of cells.
 __device__ __forceinline__ int sub_bin(float x, float lo, float inv, int nb) {
     float t = (x - lo) * inv;
     float f = floorf(t);
@@ -35,20 +35,20 @@ __device__ __forceinline__ int sub_bin(float x, float lo, float inv, int nb) {
     return (int)f;
 }
 
-// Projections of a point onto frame directions k0 .. k0+M-1: for each, the
+// Projections of a point onto frame directions 0 .. M-1: for each, the
 // sequential fma chain over the terms of fl(x[coord[t]] - mean[t]) weighted by
 // dir[k][t], with coord(c) returning coordinate c of the point.  Binning and
 // the search both use it; each value is within Frame::margin of the exact
 // projection.
 template <int M, class Coord>
-__device__ __forceinline__ void frame_project(const Frame* __restrict__ f, int k0, Coord coord, float (&s)[M]) {
+__device__ __forceinline__ void frame_project(const Frame* __restrict__ f, Coord coord, float (&s)[M]) {
 #pragma unroll
     for (int m = 0; m < M; ++m) s[m] = 0.0f;
     const int T = f->terms;
     for (int t = 0; t < T; ++t) {
         const float y = coord(f->coord[t]) - f->mean[t];
 #pragma unroll
-        for (int m = 0; m < M; ++m) s[m] = fmaf(f->dir[k0 + m][t], y, s[m]);
+        for (int m = 0; m < M; ++m) s[m] = fmaf(f->dir[m][t], y, s[m]);
     }
 }
 

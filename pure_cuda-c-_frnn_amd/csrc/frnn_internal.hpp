@@ -24,42 +24,32 @@ inline int list_capacity(int K) { return K + 96 > 160 ? K + 96 : 160; }
 
 int scan_partials_count(int n);
 
-// ---- grid frame and within-cell refinement ----------------------------------
-// First-coordinate plans grid the data on its principal directions (Frame);
-// cells holding at least kBigCell points are ordered internally by a 32 x 32
-// sub-bin key on the next two principal directions, kSubBins sub-bins per big
-// cell, and the search restricts each big cell to the sub-bins that intersect
-// its queries' windows.
-constexpr int kBigCell = 256;
-constexpr int kSubBins = 1024;
-constexpr int kSubStride = kSubBins + 1;   // per big cell: sub-bin offsets and the cell total
+// ---- grid frame ---------------------------------------------------------------
+// First-coordinate plans grid the data on its principal directions (Frame).
 constexpr int kStatBlocks = 64;        // point slices per coordinate (statistics)
 constexpr int kMaxTerms = FRNN_FRAME_TERMS;
 constexpr int kMaxPairs = kMaxTerms * (kMaxTerms + 1) / 2;   // covariance entries
 constexpr int kCovBlocks = 512;         // sampled 256-point tiles (covariance)
-constexpr int kFrameGrid = 4;           // grid directions of a frame (slots 0..3)
-constexpr int kRefDir0 = 4;             // refinement directions (slots 4, 5)
+constexpr int kFrameGrid = FRNN_FRAME_DIRS;   // grid directions of a frame
 
 struct Frame {
-    int g, cells, terms, L;             // grid directions, cells, projection terms, refinement dirs
+    int g, cells, terms;                // grid directions, cells, projection terms
     int projected;                      // 0: raw first coordinates (infinite input)
-    int nb1, nb2, fine0;                // refinement sub-bins per direction; cells of axis 0 per h
+    int fine0;                          // cells of axis 0 per cell edge h
     int res[kFrameGrid];
     int stride[kFrameGrid];
     float lo[kFrameGrid];
     float h, inv_h, margin, slack;
-    float rlo0, rlo1, rinv0, rinv1;
-    float sigma[FRNN_FRAME_DIRS];
     float h0, inv_h0;                   // axis 0's cell edge h / fine0 and fl(1/h0)
+    float sigma[kFrameGrid];
     int coord[kMaxTerms];
     float mean[kMaxTerms];
-    float dir[FRNN_FRAME_DIRS][kMaxTerms];
+    float dir[kFrameGrid][kMaxTerms];
 };
 static_assert(sizeof(Frame) == sizeof(frnn_frame_t), "Frame mirrors frnn_frame_t");
 
 struct FrameLayout {
-    size_t frame, bidx, subcnt, substart, scanpart, cov, covsum, subkey, total;   // byte offsets
-    int max_big;        // upper bound on cells with >= kBigCell points
+    size_t frame, cov, covsum, total;   // byte offsets
 };
 
 // Per-coordinate statistics of the input (fp64 accumulation): the mean is the
@@ -87,7 +77,7 @@ inline long long grid_cells(int N, int D, const frnn_plan_t& p) {
     }
     return p.cells;
 }
-FrameLayout frame_layout(int N, int D, long long cells);
+FrameLayout frame_layout();
 
 // The grid the device pipeline bins on.  Raw grids (no frame) cover the
 // reference's [0, 1] domain with res = ceil(1/r) cells of edge r per axis.
@@ -112,12 +102,9 @@ inline frnn_plan_t binning_plan(const frnn_plan_t& p, int D) {
     return q;
 }
 // Frame of a first-coordinate plan: terms, sampled covariance, principal
-// directions, grid and sub-bin geometry.  Needs the point statistics.
+// directions and grid geometry.  Needs the point statistics.
 int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long long cells,
                  const void* stats_ws, void* ws, hipStream_t s);
-// Sub-bin counting of big cells (after the scan).
-int launch_refine(const float* pts, int N, int D, long long cells, const int* cell_of, const int* cnt,
-                  int* rank, void* ws, hipStream_t s);
 
 // Launchers return 0, 1 (bad argument), 2 (size limit) or 3 (HIP launch error;
 // the error code is kept for last_launch_error()).
@@ -130,14 +117,11 @@ int launch_fill_i32(int* p, long long n, int v, hipStream_t s);
 // coordinates
 int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, const void* frame_ws,
                      int cells, int* cell_of, int* rank, int* cnt, hipStream_t s);
-// flag_min > 0 scans (in[i] >= flag_min) instead of in[i]
-int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s, int flag_min = 0);
-// frame_ws: the frame workspace (refined big cells), or nullptr.  With
-// frows (which needs stats_ws) the centred filter rows fl(x - mean) are
+int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s);
+// With frows (which needs stats_ws) the centred filter rows fl(x - mean) are
 // written too.
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,
-                   const int* cnt, const void* frame_ws, long long cells, int* sorted_idx, int* inv,
-                   float* aos, const void* stats_ws, float* frows, hipStream_t s);
+                   int* sorted_idx, int* inv, float* aos, const void* stats_ws, float* frows, hipStream_t s);
 int launch_transpose(const float* pts, int N, int D, float* aos, const void* stats_ws, float* frows,
                      hipStream_t s);
 // Wide rows (padded length >= 64) stream precomputed centred filter rows;

@@ -9,10 +9,11 @@
 //   * a wave owns 32 consecutive queries of the cell-sorted order (grid paths)
 //     or of the original order (brute force);
 //   * for grid paths the wave walks, for each run of its queries sharing a
-//     row (the cells of equal coordinates on axes 1..g-1), the cells x-1..x+1
-//     around the run's queries in the 3^(g-1) neighbouring rows, skipping
-//     cells whose box is farther than every query's threshold (and, inside
-//     refined big cells, sub-bins outside the run's projection window);
+//     row (the cells of equal coordinates on axes 1..g-1), the 3^(g-1)
+//     neighbouring rows, skipping rows whose box is farther than every
+//     query's threshold; in each row it streams the cells x-1..x+1 around the
+//     run's queries (raw grids) or, on a frame's fine axis 0, the one stretch
+//     of cells that the run's threshold can still reach;
 //   * candidates stream through in tiles of 32.  The distance tile
 //     32 candidates x 32 queries is one chain of v_mfma_f32_32x32x2f32 on the
 //     augmented vectors  a = [p', |p'|^2, 1],  b = [-2q', 1-c, (1-c)|q'|^2]
@@ -108,8 +109,6 @@ struct SearchArgs {
     const int* cell_of;          // original index -> cell id (grid paths)
     const int* start;            // cells+1 exclusive cell offsets (grid paths)
     const Frame* frame;          // first-coordinate grid frame, or nullptr (raw grid)
-    const int* bidx;             // big-cell index (exclusive scan of big flags)
-    const int* substart;         // sub-bin offsets within each big cell (kSubStride per cell)
     unsigned long long* lists;   // [N][cap] candidate keys
     unsigned long long* counters;
     int N, D, K, cap, G, res;    // res: raw-grid cells per axis
@@ -781,7 +780,7 @@ void search_kernel(SearchArgs a) {
         const float* qrow = query_row(qvalid ? n : 0);
         if (proj) {
             float sp[kFrameGrid];
-            frame_project(fr, 0, [&](int d) { return qrow[d]; }, sp);
+            frame_project(fr, [&](int d) { return qrow[d]; }, sp);
             if (h == 0) {
 #pragma unroll
                 for (int d = 0; d < kFrameGrid; ++d)
@@ -1026,11 +1025,7 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     a.cell = bf ? 1.0f : plan.cell_size;
     a.radius = plan.cell_size;
     if (frame_ws && !bf) {
-        const FrameLayout L = frame_layout(N, D, grid_cells(N, D, plan));
-        const char* base = static_cast<const char*>(frame_ws);
-        a.frame = reinterpret_cast<const Frame*>(base + L.frame);
-        a.bidx = reinterpret_cast<const int*>(base + L.bidx);
-        a.substart = reinterpret_cast<const int*>(base + L.substart);
+        a.frame = reinterpret_cast<const Frame*>(static_cast<const char*>(frame_ws) + frame_layout().frame);
     }
     const double u = 5.9604644775390625e-08;   // 2^-24
     a.norm_scale = (float)(1.0 - (6.0 * DS + 32.0) * u);

@@ -24,11 +24,10 @@ __all__ = ["FRNNEngine", "plan", "FRNNError", "LIB_PATH", "MAX_K", "MAX_DIM", "M
 MAX_K = 128
 MAX_DIM = 128
 MAX_CELLS = 1_000_000
-NUM_STAGES = 9
+NUM_STAGES = 8
 NUM_COUNTERS = 4
 PROFILE_EVENTS, PROFILE_COUNTERS = 1, 2
-STAGE_NAMES = ("zero_fill", "stats", "frame", "bin_count", "scan", "refine", "reorder", "search",
-               "unpermute")
+STAGE_NAMES = ("zero_fill", "stats", "frame", "bin_count", "scan", "reorder", "search", "unpermute")
 PATH_NAMES = {-1: "empty", 0: "bruteforce", 1: "grid_full", 2: "grid_first"}
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -53,21 +52,17 @@ class _Plan(ctypes.Structure):
 
 
 FRAME_TERMS = 32
-FRAME_DIRS = 6
-FRAME_GRID = 4
+FRAME_DIRS = 4
 
 
 class FrameInfo(ctypes.Structure):
     """frnn_frame_t: the descriptor at the start of a frame workspace."""
     _fields_ = [("grid_dim", ctypes.c_int), ("cells", ctypes.c_int), ("terms", ctypes.c_int),
-                ("axes", ctypes.c_int), ("projected", ctypes.c_int), ("bins0", ctypes.c_int),
-                ("bins1", ctypes.c_int), ("fine0", ctypes.c_int),
-                ("res", ctypes.c_int * FRAME_GRID), ("stride", ctypes.c_int * FRAME_GRID),
-                ("lo", ctypes.c_float * FRAME_GRID), ("h", ctypes.c_float), ("inv_h", ctypes.c_float),
+                ("projected", ctypes.c_int), ("fine0", ctypes.c_int),
+                ("res", ctypes.c_int * FRAME_DIRS), ("stride", ctypes.c_int * FRAME_DIRS),
+                ("lo", ctypes.c_float * FRAME_DIRS), ("h", ctypes.c_float), ("inv_h", ctypes.c_float),
                 ("margin", ctypes.c_float), ("slack", ctypes.c_float),
-                ("rlo0", ctypes.c_float), ("rlo1", ctypes.c_float),
-                ("rinv0", ctypes.c_float), ("rinv1", ctypes.c_float),
-                ("sigma", ctypes.c_float * FRAME_DIRS), ("h0", ctypes.c_float), ("inv_h0", ctypes.c_float),
+                ("h0", ctypes.c_float), ("inv_h0", ctypes.c_float), ("sigma", ctypes.c_float * FRAME_DIRS),
                 ("coord", ctypes.c_int * FRAME_TERMS), ("mean", ctypes.c_float * FRAME_TERMS),
                 ("dir", (ctypes.c_float * FRAME_TERMS) * FRAME_DIRS)]
 
@@ -77,7 +72,7 @@ class FrameInfo(ctypes.Structure):
         return cls.from_buffer_copy(bytes(np.asarray(head, dtype=np.uint8)[:ctypes.sizeof(cls)]))
 
     def directions(self):
-        """(6, 32) float32 array of direction weights over the term coordinates."""
+        """(4, 32) float32 array of direction weights over the term coordinates."""
         return np.array([[self.dir[k][t] for t in range(FRAME_TERMS)] for k in range(FRAME_DIRS)],
                         dtype=np.float32)
 
@@ -123,8 +118,7 @@ def _load():
         "frnn_launch_point_stats": ([vp, i32, i32, vp, vp], i32),
         "frnn_frame_workspace_bytes": ([i32, i32, ctypes.POINTER(_Plan)], i64),
         "frnn_launch_frame": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp], i32),
-        "frnn_launch_refine": ([vp, i32, i32, ctypes.POINTER(_Plan), vp, vp, vp, vp, vp], i32),
-        "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp], i32),
+        "frnn_launch_reorder": ([vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp], i32),
         "frnn_launch_transpose": ([vp, i32, i32, vp, vp, vp, vp], i32),
         "frnn_uses_filter_rows": ([i32], i32),
         "frnn_launch_find_nbrs": ([vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan),

@@ -109,17 +109,14 @@ def test_launch_seam_rejects_bad_geometry_without_touching_the_device():
     p = frnn_cuda._Plan()
     assert L.frnn_make_plan(100000, 12, 32, ctypes.c_float(0.0345), ctypes.byref(p)) == 0
     assert L.frnn_launch_frame(None, 10, 12, ctypes.byref(p), None, None, None) == 1   # null pointers
-    assert L.frnn_launch_refine(None, 10, 12, ctypes.byref(p), None, None, None, None, None) == 1
     p.cells = 5
     assert L.frnn_launch_find_nbrs(None, None, None, None, None, None, None, 100000, 12, 32, ctypes.byref(p),
                                    None, 128, None, None) == 1
     assert L.frnn_launch_frame(None, 10, 12, ctypes.byref(p), None, None, None) == 1   # inconsistent plan
-    assert L.frnn_launch_refine(None, 10, 12, None, None, None, None, None, None) == 1
     q = frnn_cuda._Plan()
     assert L.frnn_make_plan(100000, 3, 16, ctypes.c_float(0.1), ctypes.byref(q)) == 0
     assert L.frnn_launch_frame(None, 10, 3, ctypes.byref(q), None, None, None) == 1     # no frame
-    assert L.frnn_launch_reorder(None, 10, 3, None, None, None, None, None, 0, None, None, None, None, None,
-                                 None) == 1
+    assert L.frnn_launch_reorder(None, 10, 3, None, None, None, None, None, None, None, None, None) == 1
     assert L.frnn_launch_transpose(None, 10, 3, None, None, None, None) == 1
     # wide rows stream precomputed centred rows; narrower ones centre in registers
     assert [L.frnn_uses_filter_rows(d) for d in (0, 3, 16, 32, 33, 64, 128, 129)] == [-1, 0, 0, 0, 1, 1, 1, -1]

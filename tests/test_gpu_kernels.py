@@ -3,8 +3,8 @@
 bin/count  vs the oracle's clamped binning and numpy bincount
 scan       vs numpy cumsum (exclusive)
 reorder    permutation / cell-order / row-copy invariants
-frame      descriptor, binning recomputed in exact fp32, the 3^g shell
-           guarantee on sampled pairs, sub-bin order inside big cells
+frame      descriptor, binning recomputed in exact fp32 (fine axis 0), the
+           3^g shell guarantee on sampled pairs
 """
 import ctypes
 
@@ -40,8 +40,8 @@ def _build(X, g, res, inv):
     sidx = t.empty(N, dtype=t.int32, device="cuda:0")
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.full((N * ds,), float("nan"), dtype=t.float32, device="cuda:0")
-    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), None, cells,
-                                 vp(sidx), vp(inv_p), vp(aos), None, None, None) == 0
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(sidx), vp(inv_p), vp(aos),
+                                 None, None, None) == 0
     t.cuda.synchronize()
     return {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start,
                                                   sidx=sidx, inv=inv_p, aos=aos).items()}
@@ -157,8 +157,8 @@ def _frame_build(X, K, radius):
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
     frows = t.empty(N * ds, dtype=t.float32, device="cuda:0")
-    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), None, cells,
-                                 vp(sidx), vp(inv_p), vp(aos), vp(sws), vp(frows), None) == 0
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(sidx), vp(inv_p), vp(aos),
+                                 vp(sws), vp(frows), None) == 0
     t.cuda.synchronize()
     out = {k: v.cpu().numpy() for k, v in dict(cell_of=cell_of, rank=rank, cnt=cnt, start=start, sidx=sidx,
                                                  inv=inv_p, aos=aos, frows=frows).items()}
@@ -188,7 +188,7 @@ def _near_pairs(X, radius, nq=400, seed=5):
 
 
 @pytest.mark.parametrize("name,N", [("metric", 300_000), ("C3", 300_000)])
-def test_frame_grid_and_refinement(name, N):
+def test_frame_grid(name, N):
     """The grid frame of first-coordinate plans: descriptor (terms, directions,
     margin, geometry with a fine axis 0), the binning recomputed in exact fp32,
     the guarantee that pairs within the radius fall in neighbouring cells of
@@ -202,8 +202,7 @@ def test_frame_grid_and_refinement(name, N):
     st = out["stats"]
     mean, var, lo, hi = (st[:, k] for k in range(4))
     T = min(w.D, 32)
-    assert fi.terms == T and fi.axes == 0      # no refinement directions with a fine axis 0
-    assert fi.bins0 * fi.bins1 == (1024 if fi.axes == 1 else 32 * 32)
+    assert fi.terms == T
     # terms: the highest-variance coordinates, lower index on ties
     coord = np.array(fi.coord[:T])
     assert np.array_equal(coord, np.argsort(-var, kind="stable")[:T])
@@ -211,7 +210,7 @@ def test_frame_grid_and_refinement(name, N):
     # directions: orthonormal up to the 1 - 2^-18 shrink; the grid block has
     # spectral norm < 1, so projected gaps lower-bound distances
     dirs = fi.directions()[:, :T].astype(np.float64)
-    slots = list(range(g)) + [4 + k for k in range(fi.axes)]
+    slots = list(range(g))
     Wm = dirs[slots]
     G = Wm @ Wm.T
     assert np.all(np.abs(np.diag(G) - 1) < 1e-5) and np.all(np.diag(G) < 1)
@@ -289,7 +288,7 @@ def test_frame_falls_back_to_raw_coordinates_on_infinite_input():
     X[17, 2] = np.inf
     out = _frame_build(X, 16, 0.1)
     fi, plan = out["frame"], out["plan"]
-    assert plan.path == 2 and fi.projected == 0 and fi.axes == 0
+    assert plan.path == 2 and fi.projected == 0
     g, F = plan.grid_dim, fi.fine0
     assert fi.cells == F * plan.cells and list(fi.res[:g]) == [F * plan.res] + [plan.res] * (g - 1)
     # the plan's cells, axis 0 split F ways: fine x, then the reference's hash
@@ -356,8 +355,8 @@ def test_seam_search_first_coordinate_plan(framed):
     inv_p = t.empty(N, dtype=t.int32, device="cuda:0")
     aos = t.empty(N * ds, dtype=t.float32, device="cuda:0")
     assert L.frnn_uses_filter_rows(D) == 0
-    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(cnt), None, cells,
-                                 vp(sidx), vp(inv_p), vp(aos), None, None, None) == 0
+    assert L.frnn_launch_reorder(vp(d), N, D, vp(cell_of), vp(rank), vp(start), vp(sidx), vp(inv_p), vp(aos),
+                                 None, None, None) == 0
     cap = frnn_cuda.list_capacity(K)
     lists = t.empty(N * cap, dtype=t.int64, device="cuda:0")
     assert L.frnn_launch_find_nbrs(vp(aos), None, vp(sws), vp(sidx), vp(cell_of), vp(start), vp(ws),
