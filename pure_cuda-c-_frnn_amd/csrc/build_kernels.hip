@@ -12,20 +12,32 @@
 //     i.e. 16-byte-aligned vector stores of whole rows instead of D scattered
 //     4-byte stores into SoA planes, and also records the inverse permutation;
 //   * the scan is a three-phase reduce/scan/propagate over 4096-element tiles
-//     with no inter-block spin waits.
+//     (16-byte coalesced accesses) with no inter-block spin waits.
 #include "frnn_device.hpp"
 #include "frnn_internal.hpp"
 
 namespace frnn {
 
 constexpr int kScanThreads = 256;
-constexpr int kScanItems = 16;
-constexpr int kScanTile = kScanThreads * kScanItems;   // 4096
+constexpr int kScanRows = 4;                              // int4 rows per thread
+constexpr int kScanTile = kScanThreads * 4 * kScanRows;   // 4096
 
+// 16-byte stores where the array is 16-byte aligned (head and tail as ints).
 __global__ void fill_i32_kernel(int* __restrict__ p, long long n, int v) {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const long long stride = (long long)gridDim.x * blockDim.x;
-    for (; i < n; i += stride) p[i] = v;
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long head = (long long)((16 - ((uintptr_t)p & 15)) & 15) / 4;
+    if (((uintptr_t)p & 3) != 0 || head >= n) {
+        for (; i < n; i += stride) p[i] = v;
+        return;
+    }
+    if (i < head) p[i] = v;
+    int4* q = reinterpret_cast<int4*>(p + head);
+    const long long nv = (n - head) / 4;
+    const int4 w = make_int4(v, v, v, v);
+    for (long long k = i; k < nv; k += stride) q[k] = w;
+    const long long t = head + 4 * nv + i;
+    if (t < n) p[t] = v;
 }
 
 // One thread per point; coordinates of the first g axes are read SoA, so a
@@ -46,78 +58,112 @@ __global__ __launch_bounds__(256) void bin_count_kernel(const float* __restrict_
     rank[i] = atomicAdd(&cnt[h], 1);
 }
 
-__device__ __forceinline__ int block_exclusive_scan_256(int v, int* s_tmp, int* total) {
-    // Hillis-Steele over 256 per-thread values in LDS.
-    const int t = threadIdx.x;
-    s_tmp[t] = v;
-    __syncthreads();
-    for (int o = 1; o < kScanThreads; o <<= 1) {
-        int x = (t >= o) ? s_tmp[t - o] : 0;
-        __syncthreads();
-        s_tmp[t] += x;
-        __syncthreads();
+// Exclusive scan in three passes over tiles of 4096 ints (256 threads x 4
+// rows of one int4; a row is 1024 consecutive ints, so every load and store
+// instruction of a wave covers 1 KB contiguously).  VEC: in and out are
+// 16-byte aligned (int4 accesses; the last partial int4 per element).
+template <bool VEC>
+__device__ __forceinline__ int4 scan_load4(const int* __restrict__ in, long long e, int n) {
+    if (VEC && e + 3 < n) return *reinterpret_cast<const int4*>(in + e);
+    return make_int4(e < n ? in[e] : 0, e + 1 < n ? in[e + 1] : 0, e + 2 < n ? in[e + 2] : 0,
+                     e + 3 < n ? in[e + 3] : 0);
+}
+
+template <bool VEC>
+__device__ __forceinline__ void scan_store4(int* __restrict__ out, long long e, int n, int4 v) {
+    if (VEC && e + 3 < n) {
+        *reinterpret_cast<int4*>(out + e) = v;
+        return;
     }
-    const int incl = s_tmp[t];
-    *total = s_tmp[kScanThreads - 1];
+    if (e < n) out[e] = v.x;
+    if (e + 1 < n) out[e + 1] = v.y;
+    if (e + 2 < n) out[e + 2] = v.z;
+    if (e + 3 < n) out[e + 3] = v.w;
+}
+
+// Exclusive scan of one int per thread over the 256-thread block: wave
+// inclusive scans (lane exchanges), then the four wave totals through LDS.
+__device__ __forceinline__ int block_exclusive_scan_256(int v, int* s_w, int* total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = threadIdx.x / kWave;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int x = __shfl_up(incl, o);
+        if (lane >= o) incl += x;
+    }
+    if (lane == kWave - 1) s_w[w] = incl;
     __syncthreads();
-    return incl - v;
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < kScanThreads / kWave; ++k) {
+        const int t = s_w[k];
+        off += k < w ? t : 0;
+        tot += t;
+    }
+    __syncthreads();   // s_w is reused by the next call
+    *total = tot;
+    return off + incl - v;
 }
 
-__device__ __forceinline__ int scan_value(const int* __restrict__ in, long long idx, int n) {
-    return idx < n ? in[idx] : 0;
-}
-
+template <bool VEC>
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int* __restrict__ in, int n,
                                                                    int* __restrict__ partials) {
-    __shared__ int s_tmp[kScanThreads];
-    const long long base = (long long)blockIdx.x * kScanTile + (long long)threadIdx.x * kScanItems;
+    __shared__ int s_w[kScanThreads / kWave];
+    const long long base = (long long)blockIdx.x * kScanTile + 4 * threadIdx.x;
     int sum = 0;
 #pragma unroll
-    for (int j = 0; j < kScanItems; ++j) sum += scan_value(in, base + j, n);
+    for (int j = 0; j < kScanRows; ++j) {
+        const int4 v = scan_load4<VEC>(in, base + j * 4 * kScanThreads, n);
+        sum += (v.x + v.y) + (v.z + v.w);
+    }
     int total;
-    block_exclusive_scan_256(sum, s_tmp, &total);
+    block_exclusive_scan_256(sum, s_w, &total);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
 
 // Single block: exclusive scan of up to kScanTile partial sums, in place.
 __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int* __restrict__ partials, int nb) {
-    __shared__ int s_tmp[kScanThreads];
-    const int base = threadIdx.x * kScanItems;
-    int v[kScanItems];
+    __shared__ int s_w[kScanThreads / kWave];
+    constexpr int kPer = kScanTile / kScanThreads;
+    const int base = threadIdx.x * kPer;
+    int v[kPer];
     int sum = 0;
 #pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
+    for (int j = 0; j < kPer; ++j) {
         v[j] = (base + j < nb) ? partials[base + j] : 0;
         sum += v[j];
     }
     int total;
-    int run = block_exclusive_scan_256(sum, s_tmp, &total);
+    int run = block_exclusive_scan_256(sum, s_w, &total);
 #pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
+    for (int j = 0; j < kPer; ++j) {
         if (base + j < nb) partials[base + j] = run;
         run += v[j];
     }
 }
 
+template <bool VEC>
 __global__ __launch_bounds__(kScanThreads) void scan_final_kernel(const int* __restrict__ in, int n,
                                                                   const int* __restrict__ partials,
                                                                   int* __restrict__ out) {
-    __shared__ int s_tmp[kScanThreads];
-    const long long base = (long long)blockIdx.x * kScanTile + (long long)threadIdx.x * kScanItems;
-    int v[kScanItems];
-    int sum = 0;
+    __shared__ int s_w[kScanThreads / kWave];
+    const long long base = (long long)blockIdx.x * kScanTile + 4 * threadIdx.x;
+    int4 v[kScanRows];
 #pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
-        v[j] = scan_value(in, base + j, n);
-        sum += v[j];
-    }
-    int total;
-    int run = block_exclusive_scan_256(sum, s_tmp, &total) + partials[blockIdx.x];
+    for (int j = 0; j < kScanRows; ++j) v[j] = scan_load4<VEC>(in, base + j * 4 * kScanThreads, n);
+    int carry = partials[blockIdx.x];
 #pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
-        long long idx = base + j;
-        if (idx < n) out[idx] = run;
-        run += v[j];
+    for (int j = 0; j < kScanRows; ++j) {
+        int total;
+        const int x = carry + block_exclusive_scan_256((v[j].x + v[j].y) + (v[j].z + v[j].w), s_w, &total);
+        int4 o;
+        o.x = x;
+        o.y = o.x + v[j].x;
+        o.z = o.y + v[j].y;
+        o.w = o.z + v[j].z;
+        scan_store4<VEC>(out, base + j * 4 * kScanThreads, n, o);
+        carry += total;
     }
 }
 
@@ -748,8 +794,8 @@ hipError_t last_launch_error() { return g_launch_error; }
 
 int launch_fill_i32(int* p, long long n, int v, hipStream_t s) {
     if (n <= 0) return 0;
-    long long nb = (n + 255) / 256;
-    if (nb > 65536) nb = 65536;
+    long long nb = (n / 4 + 255) / 256;   // one int4 per thread
+    nb = nb < 1 ? 1 : (nb > 65536 ? 65536 : nb);
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)nb), dim3(256), 0, s, p, n, v);
     return launch_result();
 }
@@ -775,9 +821,14 @@ int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStre
     if (n <= 0) return 0;
     const int nb = (n + kScanTile - 1) / kScanTile;
     if (nb > kScanTile) return 2;
-    hipLaunchKernelGGL(scan_reduce_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials);
+    const bool vec = (((uintptr_t)in | (uintptr_t)out) & 15) == 0;
+    if (vec) hipLaunchKernelGGL(scan_reduce_kernel<true>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials);
+    else hipLaunchKernelGGL(scan_reduce_kernel<false>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials);
     hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partials, nb);
-    hipLaunchKernelGGL(scan_final_kernel, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out);
+    if (vec)
+        hipLaunchKernelGGL(scan_final_kernel<true>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out);
+    else
+        hipLaunchKernelGGL(scan_final_kernel<false>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out);
     return launch_result();
 }
 

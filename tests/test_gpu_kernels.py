@@ -94,6 +94,51 @@ def test_exclusive_scan(n):
     assert np.array_equal(d_out.cpu().numpy().astype(np.int64), want)
 
 
+@pytest.mark.parametrize("n,off_in,off_out", [(4097, 1, 0), (100_003, 0, 3), (9, 2, 2), (1_000_001, 3, 1)])
+def test_exclusive_scan_unaligned(n, off_in, off_out):
+    """Arrays that are not 16-byte aligned (offset by whole ints) take the
+    per-int path; lengths that are not multiples of 4 exercise the tails."""
+    t = torch()
+    rs = np.random.RandomState(n % 997)
+    a = rs.randint(0, 64, n).astype(np.int32)
+    buf_in = t.full((n + 4,), 12345, dtype=t.int32, device="cuda:0")
+    buf_in[off_in:off_in + n] = t.from_numpy(a).to("cuda:0")
+    buf_out = t.full((n + 4,), -1, dtype=t.int32, device="cuda:0")
+    part = t.empty(frnn_cuda.scan_partials_count(n), dtype=t.int32, device="cuda:0")
+    log(f"scan unaligned n={n} off_in={off_in} off_out={off_out}")
+    assert frnn_cuda._load().frnn_launch_exclusive_scan(vp(buf_in[off_in:]), n, vp(buf_out[off_out:]),
+                                                        vp(part), None) == 0
+    t.cuda.synchronize()
+    got = buf_out.cpu().numpy()
+    want = np.concatenate([[0], np.cumsum(a.astype(np.int64))[:-1]])
+    assert np.array_equal(got[off_out:off_out + n].astype(np.int64), want)
+    assert np.all(got[:off_out] == -1) and np.all(got[off_out + n:] == -1)
+
+
+@pytest.mark.parametrize("off", [0, 1, 2, 3])
+def test_bin_count_zero_fills_unaligned_counts(off):
+    """bin/count zero-fills its count array itself (garbage before, guards
+    around it untouched), also when the array is not 16-byte aligned."""
+    t = torch()
+    rs = np.random.RandomState(7 + off)
+    N, res = 5000, 37
+    X = rs.rand(N, 2).astype(np.float32)
+    inv = float(np.float32(1.0) / np.float32(1.0 / res))
+    cells = res * res
+    d = device_soa(X)
+    buf = t.full((cells + 1 + 8,), -7, dtype=t.int32, device="cuda:0")
+    cell_of = t.empty(N, dtype=t.int32, device="cuda:0")
+    rank = t.empty(N, dtype=t.int32, device="cuda:0")
+    log(f"bin/count unaligned counts off={off}")
+    assert frnn_cuda._load().frnn_launch_bin_count(vp(d), N, 2, res, ctypes.c_float(inv), cells, None,
+                                                   vp(cell_of), vp(rank), vp(buf[off:]), None) == 0
+    t.cuda.synchronize()
+    got = buf.cpu().numpy()
+    want = np.bincount(O.bin_cells(X, 2, res, np.float32(inv)), minlength=cells + 1)
+    assert np.array_equal(got[off:off + cells + 1], want)
+    assert np.all(got[:off] == -7) and np.all(got[off + cells + 1:] == -7)
+
+
 def test_scan_rejects_oversize():
     t = torch()
     assert frnn_cuda._load().frnn_launch_exclusive_scan(None, 4096 * 4096 + 1, None, None, None) == 1
