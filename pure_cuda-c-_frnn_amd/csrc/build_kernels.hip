@@ -729,52 +729,92 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict_
 }
 
 // Output transpose through LDS, qt original queries per workgroup (64, or 32
-// for K > 64): each query's K keys (row inv[i] of the sorted order,
-// contiguous) are read as 16-byte pairs and split into index and distance
-// columns of two padded LDS tiles [k][query]; then the workgroup writes whole
-// output rows k, qt consecutive queries per store.
-// The two tiles take 2 * K * (qt + 1) * 4 bytes of dynamic LDS; pairs is set
-// when K and cap are even and lists is 16-byte aligned.
+// for K > 64): the workgroup's sorted positions inv[i] go to LDS first; each
+// query's K keys (row inv[i] of the sorted order, contiguous) are then read as
+// 16-byte pairs, kUnpermBatch per thread in flight before any is stored, and
+// split into index and distance columns of two padded LDS tiles [k][query];
+// then the workgroup writes whole output rows k, qt consecutive queries per
+// store.  Lists and outputs are touched once: nontemporal loads and stores.
+// The tiles take 2 * K * (qt + 1) * 4 bytes of dynamic LDS plus qt ints of
+// positions; pairs is set when K and cap are even and lists is 16-byte
+// aligned.
+constexpr int kUnpermBatch = 8;
+
 __global__ __launch_bounds__(256) void unpermute_kernel(const unsigned long long* __restrict__ lists,
                                                         int cap, const int* __restrict__ inv, int N,
                                                         int K, int qt, int pairs, int* __restrict__ idxs,
                                                         float* __restrict__ dists) {
+    typedef unsigned long long u64x2 __attribute__((ext_vector_type(2)));
     const int kPitch = qt + 1;
     extern __shared__ int s_dyn[];
     int* const s_idx = s_dyn;
     float* const s_d2 = reinterpret_cast<float*>(s_dyn + K * kPitch);
+    int* const s_sp = s_dyn + 2 * K * kPitch;
     const int i0 = blockIdx.x * qt;
     const int nq = min(qt, N - i0);
     const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    for (int q = tid; q < nq; q += nt) s_sp[q] = inv ? inv[i0 + q] : i0 + q;
+    __syncthreads();
+    auto put = [&](int q, int k, unsigned long long key) __attribute__((always_inline)) {
+        s_idx[k * kPitch + q] = (int)(unsigned int)key;
+        s_d2[k * kPitch + q] = key_d2(key);
+    };
     if (pairs) {
         const int half = K >> 1;   // key pairs per query
-        for (int j = tid; j < nq * half; j += blockDim.x) {
-            const int q = j / half;
-            const int k = 2 * (j - q * half);
-            const int sp = inv ? inv[i0 + q] : i0 + q;
-            const ulonglong2 kv = *reinterpret_cast<const ulonglong2*>(lists + (size_t)sp * cap + k);
-            s_idx[k * kPitch + q] = (int)(unsigned int)kv.x;
-            s_d2[k * kPitch + q] = key_d2(kv.x);
-            s_idx[(k + 1) * kPitch + q] = (int)(unsigned int)kv.y;
-            s_d2[(k + 1) * kPitch + q] = key_d2(kv.y);
+        const int total = nq * half;
+        for (int j0 = 0; j0 < total; j0 += kUnpermBatch * nt) {
+            u64x2 kv[kUnpermBatch];
+#pragma unroll
+            for (int u = 0; u < kUnpermBatch; ++u) {
+                const int j = j0 + u * nt + tid;
+                if (j < total) {
+                    const int q = j / half;
+                    const int k = 2 * (j - q * half);
+                    kv[u] = __builtin_nontemporal_load(
+                        reinterpret_cast<const u64x2*>(lists + (size_t)s_sp[q] * cap + k));
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kUnpermBatch; ++u) {
+                const int j = j0 + u * nt + tid;
+                if (j < total) {
+                    const int q = j / half;
+                    const int k = 2 * (j - q * half);
+                    put(q, k, kv[u].x);
+                    put(q, k + 1, kv[u].y);
+                }
+            }
         }
     } else {
-        for (int j = tid; j < nq * K; j += blockDim.x) {
-            const int q = j / K;
-            const int k = j - q * K;
-            const int sp = inv ? inv[i0 + q] : i0 + q;
-            const unsigned long long key = lists[(size_t)sp * cap + k];
-            s_idx[k * kPitch + q] = (int)(unsigned int)key;
-            s_d2[k * kPitch + q] = key_d2(key);
+        const int total = nq * K;
+        for (int j0 = 0; j0 < total; j0 += kUnpermBatch * nt) {
+            unsigned long long kv[kUnpermBatch];
+#pragma unroll
+            for (int u = 0; u < kUnpermBatch; ++u) {
+                const int j = j0 + u * nt + tid;
+                if (j < total) {
+                    const int q = j / K;
+                    kv[u] = __builtin_nontemporal_load(lists + (size_t)s_sp[q] * cap + (j - q * K));
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kUnpermBatch; ++u) {
+                const int j = j0 + u * nt + tid;
+                if (j < total) {
+                    const int q = j / K;
+                    put(q, j - q * K, kv[u]);
+                }
+            }
         }
     }
     __syncthreads();
-    for (int j = tid; j < K * qt; j += blockDim.x) {
+    for (int j = tid; j < K * qt; j += nt) {
         const int k = j / qt;
         const int q = j - k * qt;
         if (q < nq) {
-            idxs[(size_t)k * N + i0 + q] = s_idx[k * kPitch + q];
-            dists[(size_t)k * N + i0 + q] = s_d2[k * kPitch + q];
+            __builtin_nontemporal_store(s_idx[k * kPitch + q], &idxs[(size_t)k * N + i0 + q]);
+            __builtin_nontemporal_store(s_d2[k * kPitch + q], &dists[(size_t)k * N + i0 + q]);
         }
     }
 }
@@ -916,7 +956,7 @@ int launch_unpermute(const unsigned long long* lists, int cap, const int* inv, i
     if (K < 1 || K > FRNN_MAX_K || cap < K) return 1;   // the LDS tile holds K <= FRNN_MAX_K keys
     const int pairs = (K % 2 == 0 && cap % 2 == 0 && (reinterpret_cast<uintptr_t>(lists) & 15) == 0) ? 1 : 0;
     const int qt = K > 64 ? 32 : 64;
-    const size_t lds = (size_t)2 * K * (qt + 1) * sizeof(int);   // <= 33 KiB
+    const size_t lds = ((size_t)2 * K * (qt + 1) + qt) * sizeof(int);   // <= 33 KiB
     hipLaunchKernelGGL(unpermute_kernel, dim3(blocks_for(N, qt)), dim3(256), lds, s, lists, cap, inv, N,
                        K, qt, pairs, idxs, dists);
     return launch_result();
