@@ -198,15 +198,15 @@ void search_kernel(SearchArgs a) {
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points
     // at virtual stream positions [vbeg, vend)
     __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing];
-    // current tile, per candidate row: the sorted position and (tile-exact
-    // path) the original index and the raw row (stride RS, as s_q), and the
-    // hit entries (row << 5 | query).  At DS = 16 (four waves per SIMD) the
-    // rows are not staged, which keeps the workgroup within a quarter of the
-    // LDS per SIMD: the exact rounds read the just-gathered rows from cache.
-    constexpr bool kStageRows = kTileExact && DS != 16;
-    __shared__ int t_pos[32];
+    // current tile, per candidate row: the sorted position (queue path) or
+    // the original index and the raw row (tile-exact path), and the hit
+    // entries (row << 5 | query).  Staged rows are TS floats apart: RS as s_q, except
+    // at DS = 16 (four waves per SIMD), where unpadded rows keep the
+    // workgroup within a quarter of the LDS per SIMD.
+    constexpr int TS = DS == 16 ? DS : RS;
+    __shared__ int t_pos[kTileExact ? 1 : 32];
     __shared__ int t_idx[kTileExact ? 32 : 1];
-    __shared__ __align__(16) float t_rows[kStageRows ? 32 * RS : 4];
+    __shared__ __align__(16) float t_rows[kTileExact ? 32 * TS : 4];
     // (a tile holds at most 32 x 32 hits; 64 more entries take the writes of
     // lanes without a hit, one per lane)
     __shared__ unsigned short s_hit[kTileExact ? 32 * 32 + kWave : 2];
@@ -546,8 +546,7 @@ void search_kernel(SearchArgs a) {
         return __ballot(qvalid && mn < thr_f) != 0;
     };
 
-    // Tile-exact path: the tile's sorted positions, original indices and
-    // (kStageRows) raw rows go to LDS,
+    // Tile-exact path: the tile's original indices and raw rows go to LDS,
     // the hits (row << 5 | query) are written register by register at ballot
     // prefix offsets, and they are re-evaluated in rounds of 64 lanes, each
     // round preceded by the compaction of any list that could overflow in it.
@@ -556,10 +555,9 @@ void search_kernel(SearchArgs a) {
         if (!any_hit(acc, robust)) return;
         lds_sync();
         // both halves store the same values
-        t_pos[n] = t.pos;
         t_idx[n] = t.idx;
-        if constexpr (kStageRows) {
-            float* dst = t_rows + n * RS + h * HD;
+        {
+            float* dst = t_rows + n * TS + h * HD;
 #pragma unroll
             for (int j = 0; j < HD; ++j) dst[j] = t.op[j];
         }
@@ -613,8 +611,7 @@ void search_kernel(SearchArgs a) {
                 const int e = s_hit[base + lane];
                 const int qn = e & 31;
                 const int row = e >> 5;
-                const float* prow = kStageRows ? t_rows + row * RS : a.pts + (size_t)t_pos[row] * DS;
-                const float d2 = exact_d2<DS, REV>(s_q + qn * RS, prow);
+                const float d2 = exact_d2<DS, REV>(s_q + qn * RS, t_rows + row * TS);
                 const unsigned long long key = make_key(d2, t_idx[row]);
                 accepted = key < s_thr[qn];
                 if (accepted) {
