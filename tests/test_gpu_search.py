@@ -123,6 +123,42 @@ def test_nan_points_have_no_neighbours():
     assert np.all(gi[5] == -1) and not np.any(gi == 5)
 
 
+def _degenerate(kind):
+    rs = np.random.RandomState(17)
+    if kind == "identical":                 # one point repeated: every projection equal
+        X = np.full((3000, 12), 0.37, np.float32)
+        X[:5] += np.float32(0.01) * np.arange(5, dtype=np.float32)[:, None]
+        return X, 16, 0.1
+    if kind == "line":                      # rank 1: one principal direction carries all spread
+        u = rs.randn(12)
+        u /= np.linalg.norm(u)
+        t = rs.rand(5000)
+        return (0.5 + 0.4 * (t[:, None] - 0.5) * u[None, :]).astype(np.float32), 16, 0.1
+    if kind == "two_clusters":              # far apart relative to r: empty middle cells
+        c = np.where(rs.rand(20000) < 0.5, 0.25, 0.75)[:, None]
+        return (c + 0.008 * rs.randn(20000, 16)).astype(np.float32), 16, 0.05
+    if kind == "slab":                      # all spread on one coordinate, many points per fine cell
+        X = (1e-4 * rs.rand(20000, 8)).astype(np.float32)
+        X[:, 0] = rs.rand(20000).astype(np.float32)
+        return X, 16, 0.05
+    if kind == "gauss6":                    # full-rank data: every frame axis carries spread
+        return (0.5 + 0.1 * rs.randn(50000, 6)).astype(np.float32), 32, 0.09
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["identical", "line", "two_clusters", "slab", "gauss6"])
+def test_degenerate_frame_geometries(kind):
+    """Frames on inputs whose principal directions or spread degenerate: the
+    fine axis-0 windows and the frame geometry must still return the oracle's
+    rows on every query."""
+    X, K, r = _degenerate(kind)
+    log(f"degenerate frame {kind}: N={len(X)} D={X.shape[1]} K={K} r={r}")
+    gi, gd, plan = engine_search(X, K, r)
+    assert plan["path"] == "grid_first"
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, f"degenerate {kind}")
+
+
 def test_huge_radius_everything_in_range():
     rs = np.random.RandomState(8)
     X = rs.rand(700, 5).astype(np.float32)
