@@ -67,8 +67,11 @@ typedef struct frnn_dim_stat {
     float mean, var, lo, hi;
 } frnn_dim_stat_t;
 
-/* Grid frame of first-coordinate plans (no reference counterpart); a frame
- * workspace starts with it.  The result does not depend on the grid: every point
+/* Grid frame of grid plans with at most 4 grid axes (no reference
+ * counterpart); a frame workspace starts with it.  First-coordinate plans with
+ * dim > grid_dim get a projected frame, every other such grid plan a raw frame
+ * (projected == 0: the plan's own cells on the first grid_dim coordinates,
+ * axis 0 split fine0 ways).  The result does not depend on the grid: every point
  * within the radius of a query lies in the query's 3^g cell shell of any grid
  * whose cells are at least the radius wide (plus rounding slack), so the engine
  * grids the data along its own principal directions instead of the first g
@@ -82,9 +85,9 @@ typedef struct frnn_dim_stat {
  * c_k = clamp(floor((s_k - lo[k]) * inv_h), 0, res[k] - 1) (inv_h0 for k = 0)
  * and cell id sum_k c_k * stride[k].  Direction 0 has fine0 cells per cell edge
  * h, so the points of a row of cells (fixed c_1..c_{g-1}) are ordered by their
- * projection on it.  projected == 0 (infinite input) falls back to the first
- * grid_dim raw coordinates with the plan's cell size and resolution (axis 0
- * still split fine0 ways). */
+ * projection on it.  projected == 0 (raw frames, and projected frames on
+ * infinite input) bins the first grid_dim raw coordinates with the plan's cell
+ * size and resolution (axis 0 still split fine0 ways). */
 #define FRNN_FRAME_TERMS 32
 #define FRNN_FRAME_DIRS 4
 typedef struct frnn_frame {
@@ -181,10 +184,11 @@ int frnn_engine_counters(const frnn_engine_t* engine, long long* out, int n);
 /* ---- kernel launch seam (replaces run_*, frnn_engine.cu:9-20) ------------ */
 /* All pointers are device pointers; launches are asynchronous on `stream`. */
 
-/* Cell count a plan's grid uses: res^g, except for first-coordinate plans with
- * dim > grid_dim (which have a frame): the frame's capacity
- * fine0 * max(min(max(N, 4096), FRNN_MAX_CELLS), res^g) with fine0 = 8 (the
- * frame picks its resolution to fit), at most 8 * FRNN_MAX_CELLS.
+/* Cell count a plan's grid uses: res^g without a frame (more than 4 grid
+ * axes); fine0 * res^g with fine0 = 8 for a raw frame; for first-coordinate
+ * plans with dim > grid_dim (projected frame) the frame's capacity
+ * fine0 * max(min(max(N, 4096), FRNN_MAX_CELLS), res^g) (the frame picks its
+ * resolution to fit).  At most 8 * FRNN_MAX_CELLS.
  * Count arrays hold cells + 1 ints. */
 long long frnn_grid_cells(int N, int dim, const frnn_plan_t* plan);
 
@@ -207,11 +211,13 @@ int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partia
 long long frnn_stats_workspace_bytes(int dim);
 int frnn_launch_point_stats(const float* d_points_soa, int N, int dim, void* d_stats_ws, void* stream);
 
-/* Grid frame of first-coordinate plans (no reference counterpart;
- * frnn_frame_t).  frnn_frame_workspace_bytes() bytes at d_frame_ws (0: the plan
- * has no frame).  frnn_launch_frame writes the frame (principal directions of
- * the up to 32 highest-variance coordinates from a sampled covariance; needs
- * the point statistics); run it before binning. */
+/* Grid frame of grid plans with at most 4 grid axes (no reference
+ * counterpart; frnn_frame_t).  frnn_frame_workspace_bytes() bytes at
+ * d_frame_ws (0: the plan has no frame).  frnn_launch_frame writes the frame:
+ * for first-coordinate plans with dim > grid_dim the principal directions of
+ * the up to 32 highest-variance coordinates from a sampled covariance (needs
+ * the point statistics), otherwise the raw frame (d_stats_ws may be NULL);
+ * run it before binning. */
 long long frnn_frame_workspace_bytes(int N, int dim, const frnn_plan_t* plan);
 int frnn_launch_frame(const float* d_points_soa, int N, int dim, const frnn_plan_t* plan,
                       const void* d_stats_ws, void* d_frame_ws, void* stream);

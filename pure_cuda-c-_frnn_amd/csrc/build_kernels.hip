@@ -458,6 +458,47 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 
 constexpr int kMaxDirs = FRNN_FRAME_DIRS;
 
+// Raw-coordinate geometry: the first g coordinates on the plan's own cells
+// (origin 0, edge cell_raw, binning reciprocal inv_cell_raw, res_raw cells per
+// axis), axis 0 split fine0 ways (a power of two, so h0 and inv_h0 are exact
+// scalings and a fine cell / fine0 is the plan's cell).  No projection, so no
+// rounding margin or slack.  One thread.
+__device__ void set_raw_geometry(Frame* __restrict__ f, int g, float cell_raw, float inv_cell_raw, int res_raw,
+                                 int fine0) {
+    f->projected = 0;
+    f->fine0 = fine0;
+    f->margin = 0.0f;
+    f->slack = 0.0f;
+    f->h = cell_raw;
+    f->inv_h = inv_cell_raw;
+    f->h0 = cell_raw / (float)fine0;
+    f->inv_h0 = inv_cell_raw * (float)fine0;
+    int stride = 1;
+    for (int d = 0; d < kFrameGrid; ++d) {
+        f->res[d] = d < g ? (d == 0 ? res_raw * fine0 : res_raw) : 1;
+        f->lo[d] = 0.0f;
+        f->stride[d] = stride;
+        stride *= f->res[d];
+    }
+    f->cells = stride;
+}
+
+// Raw frame of a grid plan without a projection (one wave): no terms or
+// directions, the plan's own cells with a fine axis 0.
+__global__ __launch_bounds__(64) void raw_frame_kernel(int g, float cell_raw, float inv_cell_raw, int res_raw,
+                                                       int fine0, Frame* __restrict__ f) {
+    for (int i = threadIdx.x; i < kMaxTerms; i += blockDim.x) {
+        f->coord[i] = 0;
+        f->mean[i] = 0.0f;
+    }
+    for (int i = threadIdx.x; i < kFrameGrid * kMaxTerms; i += blockDim.x) (&f->dir[0][0])[i] = 0.0f;
+    if (threadIdx.x != 0) return;
+    f->g = g;
+    f->terms = 0;
+    for (int d = 0; d < kFrameGrid; ++d) f->sigma[d] = 0.0f;
+    set_raw_geometry(f, g, cell_raw, inv_cell_raw, res_raw, fine0);
+}
+
 // Principal directions and geometry of a frame (fp64, one wave; lane t holds
 // component t of every direction).  The g leading eigenvectors of the sampled
 // covariance C come from orthogonal iteration on (C / cmax)^8 (three
@@ -623,21 +664,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     if (!exact) {
         // infinite input: grid on the raw first g coordinates (axis 0 still
         // in fine0 cells per plan cell)
-        f->projected = 0;
-        f->margin = 0.0f;
-        f->slack = 0.0f;
-        f->h = cell_raw;
-        f->inv_h = inv_cell_raw;
-        f->h0 = cell_raw / (float)fine0;         // fine0 is a power of two: exact
-        f->inv_h0 = inv_cell_raw * (float)fine0;
-        int stride = 1;
-        for (int d = 0; d < kFrameGrid; ++d) {
-            f->res[d] = d < g ? (d == 0 ? res_raw * fine0 : res_raw) : 1;
-            f->lo[d] = 0.0f;
-            f->stride[d] = stride;
-            stride *= f->res[d];
-        }
-        f->cells = stride;
+        set_raw_geometry(f, g, cell_raw, inv_cell_raw, res_raw, fine0);
         return;
     }
     double sig[kFrameGrid];
@@ -909,6 +936,11 @@ int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long l
     const FrameLayout L = frame_layout();
     char* base = static_cast<char*>(ws);
     Frame* f = reinterpret_cast<Frame*>(base + L.frame);
+    if (!has_projected_frame(plan, D)) {
+        hipLaunchKernelGGL(raw_frame_kernel, dim3(1), dim3(kWave), 0, s, plan.grid_dim, plan.cell_size,
+                           plan.inv_cell, plan.res, kFine0, f);
+        return launch_result();
+    }
     const DimStat* st = reinterpret_cast<const DimStat*>(static_cast<const char*>(stats_ws) + stats_layout(D).dims);
     double* cov = reinterpret_cast<double*>(base + L.cov);
     hipLaunchKernelGGL(frame_terms_kernel, dim3(1), dim3(128), 0, s, st, plan.grid_dim, D, f);

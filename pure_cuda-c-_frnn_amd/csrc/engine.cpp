@@ -533,7 +533,8 @@ int frnn_launch_frame(const float* d_pts, int N, int dim, const frnn_plan_t* pla
                       void* d_frame_ws, void* stream) {
     ST_TRY(check_frame_plan(N, dim, plan));
     if (N == 0) return FRNN_OK;
-    if (!d_pts || !d_stats_ws || !d_frame_ws) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (!d_pts || !d_frame_ws || (frnn::has_projected_frame(*plan, dim) && !d_stats_ws))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
     return launch_status(frnn::launch_frame(d_pts, N, dim, *plan, frnn::grid_cells(N, dim, *plan), d_stats_ws,
                                             d_frame_ws, (hipStream_t)stream),
                          "frame launch");

@@ -60,27 +60,39 @@ struct StatsLayout { size_t dims, part, total; };
 StatsLayout stats_layout(int D);
 int launch_point_stats(const float* pts, int N, int D, void* stats_ws, hipStream_t s);
 
-inline bool has_frame(const frnn_plan_t& p, int D) { return p.path == FRNN_PATH_GRID_FIRST && D > p.grid_dim; }
-// A frame's axis 0 has kFine0 cells per cell edge h: points are ordered by
-// their projection on it inside every row of cells, so a chunk of queries
+// Grid plans with at most kFrameGrid axes bin through a frame (Frame): a
+// first-coordinate plan with D > g on its principal directions (projected
+// frame), every other one on the plan's own raw cells (raw frame).  A
+// frame's axis 0 has kFine0 cells per cell edge h: points are ordered by
+// their coordinate on it inside every row of cells, so a chunk of queries
 // covers a short stretch of its row and the search streams only the stretch
 // of each neighbouring row within reach of the chunk (all other grid axes keep
 // cells of edge h, so the rows, and the query runs sharing one, stay as long).
 constexpr int kFine0 = 8;
-// Cells (count array length - 1) of a grid plan: res^g, or the frame's
-// capacity: kFine0 x (at least res^g, which its raw-coordinate fallback uses).
+inline bool has_projected_frame(const frnn_plan_t& p, int D) {
+    return p.path == FRNN_PATH_GRID_FIRST && D > p.grid_dim;
+}
+inline bool has_frame(const frnn_plan_t& p, int D) {
+    return has_projected_frame(p, D) || ((p.path == FRNN_PATH_GRID_FULL || p.path == FRNN_PATH_GRID_FIRST) &&
+                                         p.grid_dim >= 1 && p.grid_dim <= kFrameGrid);
+}
+// Cells (count array length - 1) of a grid plan: res^g without a frame; a
+// projected frame's capacity kFine0 x max(min(max(N, 4096), 1M), res^g) (its
+// raw-coordinate fallback uses res^g); kFine0 x res^g for a raw frame.
 inline long long grid_cells(int N, int D, const frnn_plan_t& p) {
-    if (has_frame(p, D)) {
+    if (has_projected_frame(p, D)) {
         long long c = N < 4096 ? 4096 : N;
         c = c < FRNN_MAX_CELLS ? c : FRNN_MAX_CELLS;
         return (c > p.cells ? c : p.cells) * kFine0;
     }
+    if (has_frame(p, D)) return p.cells * kFine0;
     return p.cells;
 }
 FrameLayout frame_layout();
 
-// The grid the device pipeline bins on.  Raw grids (no frame) cover the
-// reference's [0, 1] domain with res = ceil(1/r) cells of edge r per axis.
+// The grid the device pipeline bins on.  Raw grids (raw frames, or no frame
+// above kFrameGrid axes) cover the reference's [0, 1] domain with
+// res = ceil(1/r) cells of edge r per axis.
 // When 1/r lies just above an integer, the last layer of cells,
 // [(res-1) r, 1], is a sliver: its rows hold a few points spread along the
 // whole row, and every such row becomes a segment of the search that streams
@@ -88,9 +100,11 @@ FrameLayout frame_layout();
 // every pruning test treats as unbounded outward, so merging a sliver
 // thinner than half a cell into the layer before it (res - 1 cells per axis,
 // the last one wider than r) keeps every pair within the radius in adjacent
-// cells.  Framed plans and all other grids are returned unchanged.
+// cells.  Plans with a projected frame and all other grids are returned
+// unchanged.
 inline frnn_plan_t binning_plan(const frnn_plan_t& p, int D) {
-    if ((p.path != FRNN_PATH_GRID_FULL && p.path != FRNN_PATH_GRID_FIRST) || has_frame(p, D) || p.res < 4)
+    if ((p.path != FRNN_PATH_GRID_FULL && p.path != FRNN_PATH_GRID_FIRST) || has_projected_frame(p, D) ||
+        p.res < 4)
         return p;
     const double r = p.cell_size;
     if ((double)(p.res - 1) * r < 1.0 - 0.5 * r) return p;
@@ -101,8 +115,9 @@ inline frnn_plan_t binning_plan(const frnn_plan_t& p, int D) {
     q.cells = c;
     return q;
 }
-// Frame of a first-coordinate plan: terms, sampled covariance, principal
-// directions and grid geometry.  Needs the point statistics.
+// Frame of a grid plan with at most kFrameGrid axes: for a projected frame
+// the terms, sampled covariance, principal directions and grid geometry
+// (needs the point statistics); for a raw frame the plan's own cells.
 int launch_frame(const float* pts, int N, int D, const frnn_plan_t& plan, long long cells,
                  const void* stats_ws, void* ws, hipStream_t s);
 

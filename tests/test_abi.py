@@ -115,7 +115,7 @@ def test_launch_seam_rejects_bad_geometry_without_touching_the_device():
     assert L.frnn_launch_frame(None, 10, 12, ctypes.byref(p), None, None, None) == 1   # inconsistent plan
     q = frnn_cuda._Plan()
     assert L.frnn_make_plan(100000, 3, 16, ctypes.c_float(0.1), ctypes.byref(q)) == 0
-    assert L.frnn_launch_frame(None, 10, 3, ctypes.byref(q), None, None, None) == 1     # no frame
+    assert L.frnn_launch_frame(None, 10, 3, ctypes.byref(q), None, None, None) == 1     # raw frame, null pointers
     assert L.frnn_launch_reorder(None, 10, 3, None, None, None, None, None, None, None, None, None) == 1
     assert L.frnn_launch_transpose(None, 10, 3, None, None, None, None) == 1
     # wide rows stream precomputed centred rows; narrower ones centre in registers
@@ -125,19 +125,25 @@ def test_launch_seam_rejects_bad_geometry_without_touching_the_device():
 
 
 def test_frame_workspace_sizes():
-    # a frame only for first-coordinate plans with dim > grid_dim
+    # a frame for every grid plan with at most 4 grid axes: projected for
+    # first-coordinate plans with dim > grid_dim, raw otherwise
     assert frnn_cuda.frame_workspace_bytes(100000, 12, 32, 0.0345) > 0     # grid_first g=4
-    assert frnn_cuda.frame_workspace_bytes(100000, 3, 16, 0.1) == 0        # full-D grid
+    assert frnn_cuda.frame_workspace_bytes(100000, 3, 16, 0.1) > 0         # full-D grid g=3 (raw)
     assert frnn_cuda.frame_workspace_bytes(200000, 128, 128, 12.96) == 0   # brute force
     assert frnn_cuda.frame_workspace_bytes(100000, 4, 8, 0.02) > 0         # grid_first g=3
+    p = frnn_cuda.plan(200000, 6, 8, 0.2)                                  # full-D grid g=6
+    assert p["path"] == "grid_full" and p["grid_dim"] == 6
+    assert frnn_cuda.frame_workspace_bytes(200000, 6, 8, 0.2) == 0
 
 
 def test_grid_cells():
-    # raw grids use res^g; a frame's capacity is 8 (its fine axis-0 cells per
-    # cell edge) x clamp(N, 4096, 1M), at least 8 x res^g
+    # a raw frame has 8 (its fine axis-0 cells per cell edge) x res^g cells,
+    # a projected frame's capacity is 8 x clamp(N, 4096, 1M), at least
+    # 8 x res^g; grids above 4 axes (no frame) use res^g
     F = 8
     p = frnn_cuda.plan(100000, 3, 16, 0.1)
-    assert frnn_cuda.grid_cells(100000, 3, 16, 0.1) == p["cells"]
+    assert frnn_cuda.grid_cells(100000, 3, 16, 0.1) == F * p["cells"]
+    assert frnn_cuda.grid_cells(200000, 6, 8, 0.2) == frnn_cuda.plan(200000, 6, 8, 0.2)["cells"]
     assert frnn_cuda.grid_cells(200000, 128, 128, 12.96) == 0
     assert frnn_cuda.grid_cells(100000, 12, 32, 0.0345) == F * max(100000, frnn_cuda.plan(100000, 12, 32, 0.0345)["cells"])
     assert frnn_cuda.grid_cells(100000, 12, 32, 0.2) == F * 100000

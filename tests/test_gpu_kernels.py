@@ -325,6 +325,27 @@ def test_frame_grid(name, N):
     log(f"  res={list(res)} h/r={fi.h / r:.3f} cells={fi.cells}")
 
 
+@pytest.mark.parametrize("D,r", [(3, 0.1), (2, 0.02), (4, 0.25)])
+def test_raw_frame_on_full_grid(D, r):
+    """Full-D grids with at most 4 axes bin through a raw frame: the plan's
+    own cells on the raw coordinates, axis 0 split 8 ways (fine cell // 8 is
+    the reference's cell coordinate)."""
+    rs = np.random.RandomState(40 + D)
+    X = rs.rand(100_000, D).astype(np.float32)
+    X[:3] = np.float32(1.0)                       # x = 1.0 clamps into the last cell
+    out = _frame_build(X, 16, r)
+    fi, plan = out["frame"], out["plan"]
+    g, F = plan.grid_dim, fi.fine0
+    assert plan.path == 1 and g == D and fi.projected == 0 and fi.terms == 0 and F == 8
+    assert fi.cells == F * plan.cells == out["cells"]
+    assert list(fi.res[:g]) == [F * plan.res] + [plan.res] * (g - 1)
+    assert np.float32(fi.h) == np.float32(plan.cell_size) and np.float32(fi.inv_h0) == np.float32(plan.inv_cell) * F
+    fine_x = np.clip(np.floor(X[:, 0] * np.float32(plan.inv_cell * F)), 0, F * plan.res - 1).astype(np.int64)
+    ref = O.bin_cells(X, g, plan.res, np.float32(plan.inv_cell))
+    assert np.array_equal(fine_x // F, ref % plan.res)
+    assert np.array_equal(out["cell_of"], fine_x + F * plan.res * (ref // plan.res))
+
+
 def test_frame_falls_back_to_raw_coordinates_on_infinite_input():
     """An infinite coordinate makes the projection bound infinite: the frame
     then bins the raw first g coordinates on the plan's own grid."""
