@@ -11,9 +11,10 @@
 //   * for grid paths the wave walks, for each run of its queries sharing a
 //     row (the cells of equal coordinates on axes 1..g-1), the 3^(g-1)
 //     neighbouring rows, skipping rows whose box is farther than every
-//     query's threshold; in each row it streams the cells x-1..x+1 around the
-//     run's queries (raw grids) or, on a frame's fine axis 0, the one stretch
-//     of cells that the run's threshold can still reach;
+//     query's threshold; in each row it streams, on a frame's fine axis 0,
+//     the one stretch of cells that the run's threshold can still reach
+//     (grids without a frame, above 4 axes: the cells x-1..x+1 around the
+//     run's queries);
 //   * candidates stream through in tiles of 32.  The distance tile
 //     32 candidates x 32 queries is one chain of v_mfma_f32_32x32x2f32 on the
 //     augmented vectors  a = [p', |p'|^2, 1],  b = [-2q', 1-c, (1-c)|q'|^2]
@@ -751,8 +752,9 @@ void search_kernel(SearchArgs a) {
         append_runs(0, lane == 0 ? a.N : 0);
         consume(true);
     } else {
-        // Grid geometry: the frame's projected axes (first-coordinate plans)
-        // or the raw coordinates on the plan's cells.  Cell ci of axis d spans
+        // Grid geometry: a projected frame's axes (first-coordinate plans with
+        // D > g), or the raw coordinates on the plan's cells (raw frames and
+        // grids without a frame).  Cell ci of axis d spans
         // [org_d + ci h_d, org_d + (ci + 1) h_d]; the binned values of its
         // points lie within slack of that span (edge cells are unbounded
         // outward, as binning clamps) and within margin of the exact
@@ -823,8 +825,9 @@ void search_kernel(SearchArgs a) {
         // at most one run per lane and streams what is available, so the tile
         // loop below is inlined once.  Items: on a frame, the 3^(g-1)
         // neighbouring rows, each contributing the stretch of its fine axis-0
-        // cells within reach of the segment (one contiguous run); on a raw
-        // grid, the cells x-1..x+1 around the segment's queries in those rows.
+        // cells within reach of the segment (one contiguous run); on a grid
+        // without a frame, the cells x-1..x+1 around the segment's queries in
+        // those rows.
         int seg = 0;
         int ib = 0, NI = 0;
         int xa = 0, nx = 1;
