@@ -65,20 +65,22 @@ def dist2(q, p, order=0):
     return acc
 
 
-def brute_force(X, K, radius, order=0):
-    """All-points FRNN on AoS X[N, D] (fp32) by exhaustive search.
+def brute_force(X, K, radius, order=0, Q=None):
+    """FRNN on AoS X[N, D] (fp32) by exhaustive search: all points as queries,
+    or the separate queries Q[M, D] against the points of X.
 
-    Returns (idx[N, K] int32, dist[N, K] float32) with rows in ascending
+    Returns (idx[M, K] int32, dist[M, K] float32) with rows in ascending
     (d2, idx) order and (r2, -1) padding.  Quadratic memory: small N only.
     """
     X = np.asarray(X, dtype=np.float32)
-    N = X.shape[0]
+    Q = X if Q is None else np.asarray(Q, dtype=np.float32)
+    N, M = X.shape[0], Q.shape[0]
     r2 = np.float32(np.float32(radius) * np.float32(radius))
-    E = dist2(X[:, None, :], X[None, :, :], order)          # [N, N]
-    idx = np.full((N, K), -1, dtype=np.int32)
-    dist = np.full((N, K), r2, dtype=np.float32)
+    E = dist2(Q[:, None, :], X[None, :, :], order)          # [M, N]
+    idx = np.full((M, K), -1, dtype=np.int32)
+    dist = np.full((M, K), r2, dtype=np.float32)
     cols = np.arange(N)
-    for i in range(N):
+    for i in range(M):
         row = E[i]
         m = row < r2
         cand = cols[m]

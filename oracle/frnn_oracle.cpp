@@ -133,7 +133,7 @@ struct Grid {
     std::vector<float> aos;     // AoS coords in original order [i*D + d]
 };
 
-void build_grid(const float* soa, int N, int D, const Plan& p, Grid& G) {
+void build_grid(const float* soa, int N, const Plan& p, Grid& G) {
     G.cell_of.assign(N, 0);
     G.start.assign((size_t)p.cells + 1, 0);
     for (int i = 0; i < N; ++i) {
@@ -166,8 +166,7 @@ void finish_row(std::vector<Cand>& c, int K, float r2, int* idx_row, float* dist
     }
 }
 
-void query_bf(const std::vector<float>& aos, int N, int D, int qi, float r2, std::vector<Cand>& c) {
-    const float* q = &aos[(size_t)qi * D];
+void query_bf(const std::vector<float>& aos, int N, int D, const float* q, float r2, std::vector<Cand>& c) {
     c.clear();
     for (int j = 0; j < N; ++j) {
         float e = dist2_fwd(q, &aos[(size_t)j * D], D);
@@ -175,9 +174,8 @@ void query_bf(const std::vector<float>& aos, int N, int D, int qi, float r2, std
     }
 }
 
-void query_grid(const std::vector<float>& aos, int N, int D, const Plan& p, const Grid& G,
-                int qi, std::vector<Cand>& c) {
-    const float* q = &aos[(size_t)qi * D];
+void query_grid(const std::vector<float>& aos, int D, const Plan& p, const Grid& G, const float* q,
+                std::vector<Cand>& c) {
     int qc[16];
     for (int d = 0; d < p.g; ++d) qc[d] = bin_coord(q[d], p.inv_cell, p.res);
     long long nshell = 1;
@@ -251,7 +249,7 @@ int oracle_search(const float* soa, int N, int D, int K, float radius, int force
     std::vector<float> aos;
     to_aos(soa, N, D, aos);
     Grid G;
-    if (p.path != PATH_BF) build_grid(soa, N, D, p, G);
+    if (p.path != PATH_BF) build_grid(soa, N, p, G);
     auto t1 = std::chrono::steady_clock::now();
 
     const bool all = (query_ids == nullptr);
@@ -262,8 +260,9 @@ int oracle_search(const float* soa, int N, int D, int K, float radius, int force
 #pragma omp for schedule(dynamic, 16)
         for (int j = 0; j < Q; ++j) {
             const int qi = all ? j : query_ids[j];
-            if (p.path == PATH_BF) query_bf(aos, N, D, qi, p.r2, c);
-            else query_grid(aos, N, D, p, G, qi, c);
+            const float* q = &aos[(size_t)qi * D];
+            if (p.path == PATH_BF) query_bf(aos, N, D, q, p.r2, c);
+            else query_grid(aos, D, p, G, q, c);
             if (all) finish_row(c, K, p.r2, idx_out + qi, dist_out + qi, N);
             else finish_row(c, K, p.r2, idx_out + (size_t)j * K, dist_out + (size_t)j * K, 1);
         }
@@ -276,6 +275,38 @@ int oracle_search(const float* soa, int N, int D, int K, float radius, int force
     return 0;
 }
 
+// Queries distinct from the points: the reference kernels' two-array form
+// (run_find_nbrs with d_points1 != d_points2, find_nbrs.cu:562-567;
+// run_bruteforce with p1 != p2, no_grid_frnn.cu:273-276).  The plan and the
+// grid are the points' own (N points); every query is binned with the same
+// parameters and scans its 3^g shell of the points' grid, or all N points on
+// a brute-force plan.  Output rows [j*K + k] for the M queries.
+int oracle_search_queries(const float* soa_p, int N, const float* soa_q, int M, int D, int K, float radius,
+                          int force_path, int nthreads, int* idx_out, float* dist_out) {
+    if (N <= 0 || M < 0 || D <= 0 || K <= 0) return 1;
+    Plan p = make_plan(N, D, K, radius);
+    if (force_path == PATH_BF) { p.path = PATH_BF; p.rev = 0; }
+    else if (force_path > 0 && p.path == PATH_BF) return 2;
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+    std::vector<float> aos, qaos;
+    to_aos(soa_p, N, D, aos);
+    to_aos(soa_q, M, D, qaos);
+    Grid G;
+    if (p.path != PATH_BF) build_grid(soa_p, N, p, G);
+#pragma omp parallel
+    {
+        std::vector<Cand> c;
+#pragma omp for schedule(dynamic, 16)
+        for (int j = 0; j < M; ++j) {
+            const float* q = &qaos[(size_t)j * D];
+            if (p.path == PATH_BF) query_bf(aos, N, D, q, p.r2, c);
+            else query_grid(aos, D, p, G, q, c);
+            finish_row(c, K, p.r2, idx_out + (size_t)j * K, dist_out + (size_t)j * K, 1);
+        }
+    }
+    return 0;
+}
+
 // Number of shell candidates (points in the 3^g cells around each query, no
 // pruning) summed over the given queries; the work measure used for the grid
 // search roofline.  Returns -1 for brute-force plans.
@@ -284,7 +315,7 @@ long long oracle_shell_candidates(const float* soa, int N, int D, int K, float r
     Plan p = make_plan(N, D, K, radius);
     if (p.path == PATH_BF || p.path == PATH_EMPTY) return -1;
     Grid G;
-    build_grid(soa, N, D, p, G);
+    build_grid(soa, N, p, G);
     long long total = 0;
     const bool all = (query_ids == nullptr);
     const int Q = all ? N : nq;

@@ -39,6 +39,8 @@ def lib():
         L.oracle_dist2.restype = f32
         L.oracle_search.argtypes = [vp, i32, i32, i32, f32, i32, i32, vp, i32, vp, vp, vp]
         L.oracle_search.restype = i32
+        L.oracle_search_queries.argtypes = [vp, i32, vp, i32, i32, i32, f32, i32, i32, vp, vp]
+        L.oracle_search_queries.restype = i32
         L.oracle_shell_candidates.argtypes = [vp, i32, i32, i32, f32, vp, i32]
         L.oracle_shell_candidates.restype = i64
         _lib = L
@@ -98,6 +100,29 @@ def search(X, K, radius, force_path=-1, nthreads=0, query_ids=None, timings=None
         raise ValueError(f"oracle_search failed with code {rc}")
     if timings is not None:
         timings.extend([float(t[0]), float(t[1])])
+    return idx, dist
+
+
+def search_queries(P, Q, K, radius, force_path=-1, nthreads=0):
+    """Oracle FRNN of the queries Q[M, D] against the points P[N, D] (the
+    reference kernels' two-array form; plan and grid are the points').
+
+    Returns (idx, dist) as [M, K] arrays, rows in ascending (d2, idx) order,
+    padding (r2, -1); indices refer to rows of P.
+    """
+    P = np.asarray(P, dtype=np.float32)
+    Q = np.asarray(Q, dtype=np.float32)
+    N, D = P.shape
+    M = Q.shape[0]
+    assert Q.shape[1] == D
+    sp = np.ascontiguousarray(P.T)
+    sq = np.ascontiguousarray(Q.T) if M else np.zeros((D, 1), np.float32)
+    idx = np.empty((M, K), dtype=np.int32)
+    dist = np.empty((M, K), dtype=np.float32)
+    rc = lib().oracle_search_queries(_ptr(sp), N, _ptr(sq), M, D, int(K), float(radius), int(force_path),
+                                     int(nthreads), _ptr(idx), _ptr(dist))
+    if rc != 0:
+        raise ValueError(f"oracle_search_queries failed with code {rc}")
     return idx, dist
 
 

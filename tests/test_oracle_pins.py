@@ -195,6 +195,35 @@ def test_oracle_matches_exact_bruteforce(label, D, k, N, r, K, path):
     assert np.array_equal(bi, fi) and np.array_equal(bd, fd), label
 
 
+def separate_queries(X, M, seed):
+    """Queries for a point set X: fresh points from a nearby cloud, exact
+    copies of some points (d2 = 0 matches), and a few outside [0, 1]."""
+    rs = np.random.RandomState(seed)
+    N, D = X.shape
+    Q = X[rs.randint(0, N, M)] + (0.02 * rs.standard_normal((M, D))).astype(np.float32)
+    Q[: M // 8] = X[rs.randint(0, N, M // 8)]
+    Q[M // 8: M // 8 + 3] += np.float32(1.5)
+    return Q.astype(np.float32)
+
+
+@pytest.mark.parametrize("label,D,k,N,r,K,path", CASES)
+def test_oracle_queries_match_exact_bruteforce(label, D, k, N, r, K, path):
+    # queries distinct from the points: the points' plan and grid, each query
+    # binned with the same parameters (clamped), against an exhaustive search
+    X = unit_cloud(N, D, k, 11)
+    Q = separate_queries(X, 300, 5)
+    p = O.plan(N, D, K, r)
+    assert p["path"] == path
+    gi, gd = O.search_queries(X, Q, K, r)
+    ni, nd = E.brute_force(X, K, r, order=p["rev_order"], Q=Q)
+    assert np.array_equal(gi, ni), label
+    assert np.array_equal(gd, nd), label
+    # the all-points search is the special case Q = X
+    si, sd = O.search_queries(X, X, K, r)
+    ai, ad = O.search(X, K, r)
+    assert np.array_equal(si, ai) and np.array_equal(sd, ad), label
+
+
 def test_oracle_paths_cover_grid_first():
     X = unit_cloud(20000, 12, 3, 12)
     assert O.plan(20000, 12, 32, 0.1)["path"] == "grid_first"
