@@ -143,6 +143,18 @@ int frnn_engine_max_points(const frnn_engine_t* engine, int* out);
 int frnn_engine_search_gpu(frnn_engine_t* engine, const float* d_points_soa, int N, int dim,
                            int K, float radius, int** d_idxs, float** d_dists);
 
+/* Queries distinct from the points: the two-array form of the reference's
+ * kernels (run_find_nbrs with d_points1 != d_points2, find_nbrs.cu:562-567;
+ * run_bruteforce with p1 != p2, no_grid_frnn.cu:273-276), which its engine
+ * only ever calls with the same array.  The plan and the grid are the N
+ * points' (frnn_make_plan(N, ...)); every query is binned with the same
+ * parameters.  d_queries_soa is SoA [d*M + j], M <= max_points; outputs are
+ * engine-owned SoA [k*M + j] with indices into the points, valid until the
+ * next search.  N == 0 gives padding rows.  Synchronous. */
+int frnn_engine_search_gpu_queries(frnn_engine_t* engine, const float* d_points_soa, int N,
+                                   const float* d_queries_soa, int M, int dim, int K, float radius,
+                                   int** d_idxs, float** d_dists);
+
 /* FRNNEngine::search, frnn_engine.cu:104-193.  Host AoS points [i*dim + d] with
  * n_values = max_points * dim; N is max_points as in the reference
  * (frnn_engine.cu:108-109).  Outputs are host AoS [i*K + k], n_values/dim*K each. */
@@ -165,7 +177,8 @@ int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
  * events; FRNN_PROFILE_COUNTERS runs the counting build of the search kernel
  * and reads its work counters back after each search (0: neither).  Stages:
  * 0 zero-fill, 1 point statistics, 2 grid frame, 3 bin+count, 4 scan,
- * 5 reorder/transpose, 6 neighbour search, 7 unpermute. */
+ * 5 reorder/transpose (and, for separate queries, their binning, scan and
+ * reorder), 6 neighbour search, 7 unpermute. */
 #define FRNN_NUM_STAGES 8
 #define FRNN_PROFILE_EVENTS 1
 #define FRNN_PROFILE_COUNTERS 2

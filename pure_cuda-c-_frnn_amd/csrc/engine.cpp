@@ -109,6 +109,19 @@ struct frnn_engine {
     size_t lists_bytes = 0;
     float* h2d_points = nullptr;  // search() staging (frnn_engine.cu:27 d_points)
     size_t h2d_bytes = 0;
+    // separate queries (search_gpu_queries): binned on the points' grid and
+    // reordered into their own search order; allocated on first use
+    int* q_cell_of = nullptr;
+    int* q_rank = nullptr;
+    int* q_sorted_idx = nullptr;
+    int* q_inv = nullptr;
+    size_t q_cell_bytes = 0, q_rank_bytes = 0, q_sorted_bytes = 0, q_inv_bytes = 0;
+    int* q_start = nullptr;
+    size_t q_start_bytes = 0;
+    float* q_aos = nullptr;
+    size_t q_aos_bytes = 0;
+    float* q_frows = nullptr;
+    size_t q_frows_bytes = 0;
     frnn_plan_t last_plan{};
     bool has_result = false;
     int last_N = 0, last_K = 0;
@@ -121,18 +134,30 @@ struct frnn_engine {
 
 namespace {
 
+unsigned float_bits(float f) {
+    unsigned u;
+    std::memcpy(&u, &f, sizeof(u));
+    return u;
+}
+
 void release(frnn_engine* e) {
     void* bufs[] = {e->cell_of, e->rank, e->sorted_idx, e->inv, e->cnt, e->start, e->partials,
                     e->counters, e->out_idx, e->out_dist, e->aos, e->lists, e->h2d_points,
-                    e->frame_ws, e->stats_ws, e->frows};
+                    e->frame_ws, e->stats_ws, e->frows, e->q_cell_of, e->q_rank, e->q_sorted_idx,
+                    e->q_inv, e->q_start, e->q_aos, e->q_frows};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (auto& ev : e->ev)
         if (ev) (void)hipEventDestroy(ev);
 }
 
-// The whole device pipeline of search_gpu on an SoA device input.
-int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius) {
+// The whole device pipeline on an SoA device input: the all-points search of
+// search_gpu (d_q == nullptr), or the M queries d_q (SoA [d*M + j]) against
+// the N points (search_gpu_queries).
+int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius,
+                 const float* d_q = nullptr, int M = 0) {
+    const bool sep = d_q != nullptr;
+    const int Mq = sep ? M : N;   // queries = result rows
     frnn_plan_t ref_plan;
     ST_TRY(frnn_make_plan(N, dim, K, radius, &ref_plan));
     e->last_plan = ref_plan;
@@ -140,7 +165,7 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     // sliver of a last cell layer merged)
     const frnn_plan_t plan = frnn::binning_plan(ref_plan, dim);
     e->has_result = false;
-    if (plan.path == FRNN_PATH_EMPTY) {
+    if (plan.path == FRNN_PATH_EMPTY || Mq == 0) {
         e->has_result = true;
         e->last_N = 0;
         e->last_K = K;
@@ -149,7 +174,7 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     const int ds = frnn::aos_stride(dim);
     const int cap = frnn::list_capacity(K);
     ST_TRY(grow(&e->aos, &e->aos_bytes, (size_t)N * ds, "allocating AoS point rows"));
-    ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)N * cap, "allocating candidate lists"));
+    ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)Mq * cap, "allocating candidate lists"));
     ST_TRY(grow((char**)&e->stats_ws, &e->stats_bytes, frnn::stats_layout(dim).total, "allocating statistics"));
     float* frows = nullptr;
     if (frnn::uses_filter_rows(dim)) {
@@ -206,17 +231,51 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     else
         ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, e->stats_ws, frows, s),
                              "transpose launch"));
+    // separate queries (part of stage 5): binned on the points' grid (the
+    // count array is free again after the scan), scanned and reordered into
+    // their own search order, or transposed for brute force; their filter
+    // rows are centred on the points' mean, as the points' are
+    frnn::QuerySet qs{};
+    if (sep) {
+        ST_TRY(grow(&e->q_aos, &e->q_aos_bytes, (size_t)M * ds, "allocating query rows"));
+        float* q_frows = nullptr;
+        if (frows) {
+            ST_TRY(grow(&e->q_frows, &e->q_frows_bytes, (size_t)M * ds, "allocating query filter rows"));
+            q_frows = e->q_frows;
+        }
+        if (grid) {
+            ST_TRY(grow(&e->q_cell_of, &e->q_cell_bytes, (size_t)M, "allocating query cells"));
+            ST_TRY(grow(&e->q_rank, &e->q_rank_bytes, (size_t)M, "allocating query ranks"));
+            ST_TRY(grow(&e->q_sorted_idx, &e->q_sorted_bytes, (size_t)M, "allocating query order"));
+            ST_TRY(grow(&e->q_inv, &e->q_inv_bytes, (size_t)M, "allocating query positions"));
+            ST_TRY(grow(&e->q_start, &e->q_start_bytes, (size_t)cells + 1, "allocating query cell starts"));
+            ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, cells + 1, 0, s), "zero-fill query cells"));
+            ST_TRY(launch_status(frnn::launch_bin_count(d_q, M, plan.grid_dim, plan.res, plan.inv_cell, frame,
+                                                        (int)cells, e->q_cell_of, e->q_rank, e->cnt, s),
+                                 "query bin/count launch"));
+            ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)cells + 1, e->q_start, e->partials, s),
+                                 "query scan launch"));
+            ST_TRY(launch_status(frnn::launch_reorder(d_q, M, dim, e->q_cell_of, e->q_rank, e->q_start,
+                                                      e->q_sorted_idx, e->q_inv, e->q_aos, e->stats_ws, q_frows,
+                                                      s),
+                                 "query reorder launch"));
+        } else {
+            ST_TRY(launch_status(frnn::launch_transpose(d_q, M, dim, e->q_aos, e->stats_ws, q_frows, s),
+                                 "query transpose launch"));
+        }
+        qs = frnn::QuerySet{e->q_aos, q_frows, grid ? e->q_sorted_idx : nullptr, grid ? e->q_cell_of : nullptr, M};
+    }
     ST_TRY(mark(6));
     // stage 6: neighbour search
     ST_TRY(launch_status(frnn::launch_search(e->aos, frows, e->stats_ws, grid ? e->sorted_idx : nullptr,
                                              grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
                                              N, dim, K, plan, e->lists, cap,
-                                             e->counting ? e->counters : nullptr, s),
+                                             e->counting ? e->counters : nullptr, s, sep ? &qs : nullptr),
                          "search launch"));
     ST_TRY(mark(7));
     // stage 7: results to the original query order (ScatterToOrigKernel)
-    ST_TRY(launch_status(frnn::launch_unpermute(e->lists, cap, grid ? e->inv : nullptr, N, K,
-                                                e->out_idx, e->out_dist, s),
+    const int* qinv = grid ? (sep ? e->q_inv : e->inv) : nullptr;
+    ST_TRY(launch_status(frnn::launch_unpermute(e->lists, cap, qinv, Mq, K, e->out_idx, e->out_dist, s),
                          "unpermute launch"));
     ST_TRY(mark(8));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
@@ -231,7 +290,7 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
             return fail(FRNN_ERR_HIP, "internal list/queue capacity overflow in the search kernel");
     }
     e->has_result = true;
-    e->last_N = N;
+    e->last_N = Mq;
     e->last_K = K;
     return FRNN_OK;
 }
@@ -389,6 +448,33 @@ int frnn_engine_search_gpu(frnn_engine_t* e, const float* d_pts, int N, int dim,
     ST_TRY(frnn_validate(e->max_p, N, dim, K, radius));
     if (!d_pts && N > 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device points");
     ST_TRY(run_pipeline(e, d_pts, N, dim, K, radius));
+    if (d_idxs) *d_idxs = e->out_idx;
+    if (d_dists) *d_dists = e->out_dist;
+    return FRNN_OK;
+}
+
+int frnn_engine_search_gpu_queries(frnn_engine_t* e, const float* d_pts, int N, const float* d_queries, int M,
+                                   int dim, int K, float radius, int** d_idxs, float** d_dists) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    ST_TRY(frnn_validate(e->max_p, N, dim, K, radius));
+    if (M < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "M must be >= 0");
+    if (M > e->max_p) return fail(FRNN_ERR_CAPACITY, "M exceeds max_points");
+    if ((!d_pts && N > 0) || (!d_queries && M > 0)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (N == 0 && M > 0) {
+        // no points: every query row is padding
+        frnn_plan_t p{};
+        p.r2 = radius * radius;
+        ST_TRY(launch_status(frnn::launch_fill_i32(e->out_idx, (long long)M * K, -1, e->stream), "padding"));
+        ST_TRY(launch_status(frnn::launch_fill_i32(reinterpret_cast<int*>(e->out_dist), (long long)M * K,
+                                                   (int)float_bits(p.r2), e->stream),
+                             "padding"));
+        HIP_TRY(hipStreamSynchronize(e->stream), "padding");
+        e->has_result = true;
+        e->last_N = M;
+        e->last_K = K;
+    } else {
+        ST_TRY(run_pipeline(e, d_pts, N, dim, K, radius, d_queries ? d_queries : d_pts, M));
+    }
     if (d_idxs) *d_idxs = e->out_idx;
     if (d_dists) *d_dists = e->out_dist;
     return FRNN_OK;

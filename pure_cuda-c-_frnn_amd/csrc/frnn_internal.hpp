@@ -146,9 +146,21 @@ int launch_unpermute(const unsigned long long* lists, int cap, const int* inv, i
                      float* dists, hipStream_t s);
 // stats_ws: the point statistics (the per-coordinate means centre the MFMA
 // filter operands).
+// Queries distinct from the points, in search order: AoS rows (stride
+// aos_stride(D)), centred rows (wide rows only), search position -> original
+// query and original query -> cell id on the points' grid (grid paths).
+struct QuerySet {
+    const float* aos;
+    const float* frows;
+    const int* sorted_idx;
+    const int* cell_of;
+    int M;
+};
+// queries == nullptr: every point is a query (the all-points search).
 int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
                   const int* cell_of,
                   const int* start, const void* frame_ws, int N, int D, int K, const frnn_plan_t& plan,
-                  unsigned long long* lists, int cap, unsigned long long* counters, hipStream_t s);
+                  unsigned long long* lists, int cap, unsigned long long* counters, hipStream_t s,
+                  const QuerySet* queries = nullptr);
 
 }  // namespace frnn

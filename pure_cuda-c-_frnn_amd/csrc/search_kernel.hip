@@ -109,10 +109,17 @@ struct SearchArgs {
     const int* sorted_idx;       // sorted position -> original index (grid paths)
     const int* cell_of;          // original index -> cell id (grid paths)
     const int* start;            // cells+1 exclusive cell offsets (grid paths)
-    const Frame* frame;          // first-coordinate grid frame, or nullptr (raw grid)
-    unsigned long long* lists;   // [N][cap] candidate keys
+    const Frame* frame;          // grid frame, or nullptr (grids above 4 axes)
+    // the queries in search order (the points themselves for an all-points
+    // search): AoS rows, centred rows (wide rows only), search position ->
+    // original query index and original query index -> cell id (grid paths)
+    const float* qpts;
+    const float* qfrows;
+    const int* qsorted_idx;
+    const int* qcell_of;
+    unsigned long long* lists;   // [M][cap] candidate keys
     unsigned long long* counters;
-    int N, D, K, cap, G, res;    // res: raw-grid cells per axis
+    int N, M, D, K, cap, G, res; // N points, M queries; res: raw-grid cells per axis
     int gstride[kMaxG];          // raw-grid cell-id stride per axis
     int room;                    // usable list entries: min(cap, largest register sort)
     float r2, cell, radius;      // cell: raw-grid cell edge
@@ -232,12 +239,12 @@ void search_kernel(SearchArgs a) {
     const int chunk = blockIdx.x;
     if (chunk >= a.nchunks) return;
     const int q0 = chunk * kQB;
-    const int nq = min(kQB, a.N - q0);
+    const int nq = min(kQB, a.M - q0);
     const bool qvalid = n < nq;
     unsigned long long* const lists = a.lists + (size_t)q0 * a.cap;
 
     if constexpr (kQueryLds) {
-        const float* src = a.pts + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
+        const float* src = a.qpts + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
         float* dst = s_q + n * RS + h * HD;
 #pragma unroll
         for (int j = 0; j < HD; j += 2) {
@@ -248,7 +255,7 @@ void search_kernel(SearchArgs a) {
         }
     }
     // row of query qn (a valid query of the chunk; queue path, wide rows)
-    auto query_row = [&](int qn) -> const float* { return a.pts + (size_t)(q0 + qn) * DS; };
+    auto query_row = [&](int qn) -> const float* { return a.qpts + (size_t)(q0 + qn) * DS; };
     if (CNT && lane < 5) s_ctr[lane] = 0;
     if (lane < kQB) {
         s_cnt[lane] = 0;
@@ -277,11 +284,11 @@ void search_kernel(SearchArgs a) {
     };
     // B operand: this lane's half of query n's centred row, scaled by -2, plus
     // the norm column (the squared norm of the centred row, summed from both
-    // halves).  Rows of a chunk are the sorted points q0..q0+31.
+    // halves).  Rows of a chunk are the queries q0..q0+31 of the search order.
     float bop[HD + 1];
     float qn2 = 0.0f;
     {
-        const float* qr = op_rows + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
+        const float* qr = (kCentredRows ? a.qfrows : a.qpts) + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
         float pn = 0.0f;
 #pragma unroll
         for (int j = 0; j < HD; j += 2) {
@@ -792,7 +799,7 @@ void search_kernel(SearchArgs a) {
         // the row's x = 0 cell (rows are non-decreasing in the sorted order)
         int row_n = 0x7fffffff;
         if (qvalid) {
-            const int c = a.cell_of[a.sorted_idx[q0 + n]];
+            const int c = a.qcell_of[a.qsorted_idx[q0 + n]];
             x_n = c % res0;
             row_n = c - x_n;
         }
@@ -988,9 +995,13 @@ static void launch_ds(const SearchArgs& a, bool bf, hipStream_t s) {
 int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
                   const int* cell_of, const int* start, const void* frame_ws, int N, int D, int K,
                   const frnn_plan_t& plan, unsigned long long* lists, int cap, unsigned long long* counters,
-                  hipStream_t s) {
+                  hipStream_t s, const QuerySet* queries) {
     if (N <= 0) return 0;
     const bool bf = plan.path == FRNN_PATH_BRUTEFORCE;
+    const QuerySet self{aos, frows, sorted_idx, cell_of, N};
+    const QuerySet& Q = queries ? *queries : self;
+    if (Q.M <= 0) return 0;
+    if (!Q.aos || (!bf && (!Q.sorted_idx || !Q.cell_of)) || (uses_filter_rows(D) && !Q.frows)) return 1;
     if (!bf && (plan.grid_dim < 1 || plan.grid_dim > kMaxG || !sorted_idx || !cell_of || !start)) return 1;
     if (!bf && frame_ws && plan.grid_dim > kFrameGrid) return 1;
     if (!bf && aos_stride(D) >= 16 && plan.grid_dim > kFrameGrid) return 1;   // kernels size s_qg for g <= 4
@@ -1004,9 +1015,14 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     a.sorted_idx = sorted_idx;
     a.cell_of = cell_of;
     a.start = start;
+    a.qpts = Q.aos;
+    a.qfrows = Q.frows;
+    a.qsorted_idx = Q.sorted_idx;
+    a.qcell_of = Q.cell_of;
     a.lists = lists;
     a.counters = counters;
     a.N = N;
+    a.M = Q.M;
     a.K = K;
     a.cap = cap;
     a.room = min(cap, 4 * kWave);
@@ -1031,7 +1047,7 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     a.norm_scale = (float)(1.0 - (6.0 * DS + 32.0) * u);
     a.thr_rel = (float)(2.0 * (DS + 8.0) * u);
     a.thr_abs = 1.0e-35f;
-    a.nchunks = (N + kQB - 1) / kQB;
+    a.nchunks = (Q.M + kQB - 1) / kQB;
     if (plan.rev_order && !bf && DS == 4) {
         launch_one<4, true, false>(a, s);
     } else {

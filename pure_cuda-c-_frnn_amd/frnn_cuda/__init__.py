@@ -104,6 +104,8 @@ def _load():
         "frnn_engine_max_points": ([vp, pi32], i32),
         "frnn_engine_search_gpu": ([vp, vp, i32, i32, i32, f32, ctypes.POINTER(vp),
                                     ctypes.POINTER(vp)], i32),
+        "frnn_engine_search_gpu_queries": ([vp, vp, i32, vp, i32, i32, i32, f32, ctypes.POINTER(vp),
+                                            ctypes.POINTER(vp)], i32),
         "frnn_engine_search": ([vp, vp, i64, i32, f32, vp, vp], i32),
         "frnn_engine_get_results": ([vp, i32, i32, vp, vp], i32),
         "frnn_engine_set_stream": ([vp, vp], i32),
@@ -202,6 +204,18 @@ class FRNNEngine:
         _check(_load().frnn_engine_search_gpu(self._handle(), ctypes.c_void_p(int(dev_ptr)),
                                               int(N), int(dim), int(K), float(radius),
                                               ctypes.byref(di), ctypes.byref(dd)), "search_gpu")
+        return int(di.value or 0), int(dd.value or 0)
+
+    def search_gpu_queries(self, points_ptr, N, queries_ptr, M, dim, K, radius):
+        """Separate queries: SoA fp32 device pointers to N points p[d*N + i] and M
+        queries q[d*M + j] -> (d_idxs_ptr, d_dists_ptr), engine-owned SoA
+        [k*M + j] buffers of indices into the points (the reference kernels'
+        two-array form, find_nbrs.cu:562-567, no_grid_frnn.cu:273-276)."""
+        di, dd = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(_load().frnn_engine_search_gpu_queries(self._handle(), ctypes.c_void_p(int(points_ptr)), int(N),
+                                                      ctypes.c_void_p(int(queries_ptr)), int(M), int(dim),
+                                                      int(K), float(radius), ctypes.byref(di), ctypes.byref(dd)),
+               "search_gpu_queries")
         return int(di.value or 0), int(dd.value or 0)
 
     def get_results(self, N, K):

@@ -1,0 +1,98 @@
+"""Separate queries through the engine (GPU): M query points against N points,
+the reference kernels' two-array form (find_nbrs.cu:562-567,
+no_grid_frnn.cu:273-276), compared bit-exactly with the oracle's
+search_queries on every path."""
+import numpy as np
+import pytest
+
+import frnn_cuda
+import frnn_oracle as O
+import frnn_workloads as W
+from gpu_util import assert_rows_equal, device_soa, log
+from test_oracle_pins import CASES, separate_queries, unit_cloud
+
+pytestmark = pytest.mark.gpu
+
+
+def engine_search_queries(P, Q, K, radius, engine=None):
+    """search_gpu_queries on AoS P[N, D] and Q[M, D]; returns ([M, K] idx, [M, K] dist, plan)."""
+    P = np.asarray(P, dtype=np.float32)
+    Q = np.asarray(Q, dtype=np.float32)
+    N, D = P.shape
+    M = Q.shape[0]
+    eng = engine or frnn_cuda.FRNNEngine(max_points=max(N, M, 1))
+    dp = device_soa(P)
+    dq = device_soa(Q) if M else dp
+    eng.search_gpu_queries(dp.data_ptr(), N, dq.data_ptr(), M, D, K, radius)
+    idx, dist = eng.get_results_numpy(M, K)
+    plan = eng.last_plan()
+    if engine is None:
+        eng.close()
+    return idx.reshape(K, M).T.copy(), dist.reshape(K, M).T.copy(), plan
+
+
+@pytest.mark.parametrize("label,D,k,N,r,K,path", CASES)
+def test_queries_match_oracle(label, D, k, N, r, K, path):
+    X = unit_cloud(N, D, k, 11)
+    X[7] = X[3]
+    Q = separate_queries(X, 700, 5)
+    log(f"queries {label}: N={N} M={len(Q)} D={D} K={K} r={r}")
+    gi, gd, plan = engine_search_queries(X, Q, K, r)
+    assert plan["path"] == path
+    ri, rd = O.search_queries(X, Q, K, r)
+    assert_rows_equal(gi, gd, ri, rd, f"queries {label}")
+
+
+@pytest.mark.parametrize("M", [1, 31, 33, 5000])
+def test_query_counts_and_reuse(M):
+    # fewer and more queries than points, on one engine reused across calls
+    X = unit_cloud(3000, 12, 3, 21)
+    eng = frnn_cuda.FRNNEngine(max_points=5000)
+    Q = separate_queries(X, M, 6) if M > 1 else X[:1] + np.float32(0.001)
+    log(f"query counts M={M}")
+    for K, r in ((16, 0.1), (32, 0.15)):
+        gi, gd, _ = engine_search_queries(X, Q, K, r, engine=eng)
+        ri, rd = O.search_queries(X, Q, K, r)
+        assert_rows_equal(gi, gd, ri, rd, f"M={M} K={K}")
+    eng.close()
+
+
+def test_queries_equal_to_points_give_the_all_points_rows():
+    X = unit_cloud(4000, 16, 4, 22)
+    gi, gd, _ = engine_search_queries(X, X, 32, 0.2)
+    eng = frnn_cuda.FRNNEngine(max_points=4000)
+    d = device_soa(X)
+    eng.search_gpu(d.data_ptr(), 4000, 16, 32, 0.2)
+    ai, ad = eng.get_results_numpy(4000, 32)
+    eng.close()
+    assert np.array_equal(gi, ai.reshape(32, 4000).T)
+    assert np.array_equal(gd.view(np.uint32), ad.reshape(32, 4000).T.view(np.uint32))
+
+
+def test_empty_query_and_point_sets():
+    X = unit_cloud(500, 3, 3, 23)
+    eng = frnn_cuda.FRNNEngine(max_points=500)
+    dp = device_soa(X)
+    # no queries: nothing to return
+    eng.search_gpu_queries(dp.data_ptr(), 500, dp.data_ptr(), 0, 3, 8, 0.1)
+    assert eng.get_results_numpy(0, 8)[0].size == 0
+    # no points: every query row is padding (r2, -1)
+    eng.search_gpu_queries(dp.data_ptr(), 0, dp.data_ptr(), 500, 3, 8, 0.1)
+    idx, dist = eng.get_results_numpy(500, 8)
+    assert np.all(idx == -1) and np.all(dist == np.float32(np.float32(0.1) * np.float32(0.1)))
+    with pytest.raises(ValueError, match="max_points"):
+        eng.search_gpu_queries(dp.data_ptr(), 500, dp.data_ptr(), 501, 3, 8, 0.1)
+    eng.close()
+
+
+def test_metric_points_with_separate_queries_sampled():
+    # the headline point set with 20 000 queries near its points
+    w = W.config("metric")
+    rs = np.random.RandomState(77)
+    Q = w.X[rs.randint(0, w.N, 20000)] + (0.003 * rs.standard_normal((20000, 16))).astype(np.float32)
+    log(f"metric points N={w.N} with M={len(Q)} separate queries")
+    gi, gd, plan = engine_search_queries(w.X, Q, w.K, w.radius)
+    assert plan["path"] == "grid_first"
+    sel = np.sort(np.random.RandomState(3).choice(len(Q), 400, replace=False))
+    ri, rd = O.search_queries(w.X, Q[sel], w.K, w.radius)
+    assert_rows_equal(gi[sel], gd[sel], ri, rd, "metric queries sampled")
