@@ -155,6 +155,20 @@ int frnn_engine_search_gpu_queries(frnn_engine_t* engine, const float* d_points_
                                    const float* d_queries_soa, int M, int dim, int K, float radius,
                                    int** d_idxs, float** d_dists);
 
+/* Grid reuse across calls (no reference counterpart at the engine level:
+ * its kernels take a prebuilt grid, find_nbrs.cu:562-567, but its engine
+ * rebuilds on every call).  frnn_engine_build plans, bins and reorders the N
+ * points into engine-owned buffers (the input may be freed afterwards);
+ * frnn_engine_query then searches M query points against that grid, any
+ * number of times, with the K and radius of the build.  search_gpu,
+ * search_gpu_queries and search replace the built grid with their own, which
+ * frnn_engine_query reuses as well.  Outputs as frnn_engine_search_gpu_queries.
+ * frnn_engine_query before any build returns FRNN_ERR_STATE. */
+int frnn_engine_build(frnn_engine_t* engine, const float* d_points_soa, int N, int dim, int K,
+                      float radius);
+int frnn_engine_query(frnn_engine_t* engine, const float* d_queries_soa, int M, int** d_idxs,
+                      float** d_dists);
+
 /* FRNNEngine::search, frnn_engine.cu:104-193.  Host AoS points [i*dim + d] with
  * n_values = max_points * dim; N is max_points as in the reference
  * (frnn_engine.cu:108-109).  Outputs are host AoS [i*K + k], n_values/dim*K each. */

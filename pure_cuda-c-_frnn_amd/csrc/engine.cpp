@@ -84,6 +84,20 @@ int grow(T** p, size_t* have, size_t need_elems, const char* what) {
 
 }  // namespace
 
+// The points' side of a search, kept in the engine for the queries that
+// follow (this call's, or later frnn_engine_query calls): the plans, the
+// grid geometry and the filter rows.
+struct BuiltGrid {
+    bool valid = false;
+    frnn_plan_t ref_plan{}, plan{};
+    int N = 0, dim = 0, K = 0, ds = 0, cap = 0;
+    float radius = 0.0f;
+    bool grid = false;
+    long long cells = 0;
+    const void* frame = nullptr;
+    float* frows = nullptr;
+};
+
 struct frnn_engine {
     int max_p = 0;
     hipStream_t stream = nullptr;
@@ -130,6 +144,7 @@ struct frnn_engine {
     hipEvent_t ev[FRNN_NUM_STAGES + 1] = {};
     float stage_ms[FRNN_NUM_STAGES] = {};
     long long ctr[FRNN_NUM_COUNTERS] = {};
+    BuiltGrid built;          // the points' grid of the last build
 };
 
 namespace {
@@ -151,77 +166,78 @@ void release(frnn_engine* e) {
         if (ev) (void)hipEventDestroy(ev);
 }
 
-// The whole device pipeline on an SoA device input: the all-points search of
-// search_gpu (d_q == nullptr), or the M queries d_q (SoA [d*M + j]) against
-// the N points (search_gpu_queries).
-int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius,
-                 const float* d_q = nullptr, int M = 0) {
-    const bool sep = d_q != nullptr;
-    const int Mq = sep ? M : N;   // queries = result rows
-    frnn_plan_t ref_plan;
-    ST_TRY(frnn_make_plan(N, dim, K, radius, &ref_plan));
-    e->last_plan = ref_plan;
+// Stage events: every call records the stages it runs; stage_times() reads
+// the ones of the last call that ran the search.
+int mark_stage(frnn_engine* e, int i) {
+    if (e->profiling) HIP_TRY(hipEventRecord(e->ev[i], e->stream), "event record");
+    return FRNN_OK;
+}
+
+// Stages 0-5 on the N points (SoA device input): plan, statistics, frame,
+// bin + count, scan, reorder (or the brute-force AoS copy).
+int build_points(frnn_engine* e, BuiltGrid& b, const float* d_pts, int N, int dim, int K, float radius) {
+    b.valid = false;
+    ST_TRY(frnn_make_plan(N, dim, K, radius, &b.ref_plan));
+    e->last_plan = b.ref_plan;
     // the grid the kernels bin and search on (the reference's, with a
     // sliver of a last cell layer merged)
-    const frnn_plan_t plan = frnn::binning_plan(ref_plan, dim);
-    e->has_result = false;
-    if (plan.path == FRNN_PATH_EMPTY || Mq == 0) {
-        e->has_result = true;
-        e->last_N = 0;
-        e->last_K = K;
+    b.plan = frnn::binning_plan(b.ref_plan, dim);
+    b.N = N;
+    b.dim = dim;
+    b.K = K;
+    b.radius = radius;
+    b.ds = frnn::aos_stride(dim);
+    b.cap = frnn::list_capacity(K);
+    if (b.plan.path == FRNN_PATH_EMPTY) {
+        b.valid = true;
         return FRNN_OK;
     }
-    const int ds = frnn::aos_stride(dim);
-    const int cap = frnn::list_capacity(K);
+    const int ds = b.ds;
+    const frnn_plan_t& plan = b.plan;
     ST_TRY(grow(&e->aos, &e->aos_bytes, (size_t)N * ds, "allocating AoS point rows"));
-    ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)Mq * cap, "allocating candidate lists"));
     ST_TRY(grow((char**)&e->stats_ws, &e->stats_bytes, frnn::stats_layout(dim).total, "allocating statistics"));
-    float* frows = nullptr;
+    b.frows = nullptr;
     if (frnn::uses_filter_rows(dim)) {
         ST_TRY(grow(&e->frows, &e->frows_bytes, (size_t)N * ds, "allocating filter rows"));
-        frows = e->frows;
+        b.frows = e->frows;
     }
-
+    float* const frows = b.frows;
     hipStream_t s = e->stream;
-    const bool grid = plan.path != FRNN_PATH_BRUTEFORCE;
+    b.grid = plan.path != FRNN_PATH_BRUTEFORCE;
+    const bool grid = b.grid;
     const bool framed = grid && frnn::has_frame(plan, dim);
-    const long long cells = grid ? frnn::grid_cells(N, dim, plan) : 0;
-    const void* frame = nullptr;
+    b.cells = grid ? frnn::grid_cells(N, dim, plan) : 0;
+    const long long cells = b.cells;
+    b.frame = nullptr;
     if (framed) {
         ST_TRY(grow((char**)&e->frame_ws, &e->frame_bytes, frnn::frame_layout().total,
                     "allocating the grid frame"));
-        frame = e->frame_ws;
+        b.frame = e->frame_ws;
     }
-    if (e->counting)
-        ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * kCounterSlots, 0, s),
-                             "clearing counters"));
-    if (e->profiling) HIP_TRY(hipEventRecord(e->ev[0], s), "event record");
-    auto mark = [&](int i) -> int {
-        if (e->profiling) HIP_TRY(hipEventRecord(e->ev[i], s), "event record");
-        return FRNN_OK;
-    };
+    const void* const frame = b.frame;
+    ST_TRY(mark_stage(e, 0));
     // stage 0: zero-fill the counts (frnn_engine.cu:89-90)
     if (grid) ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, cells + 1, 0, s), "zero-fill cells"));
-    ST_TRY(mark(1));
+    ST_TRY(mark_stage(e, 1));
     // stage 1: per-coordinate statistics (filter centre, frame terms)
     ST_TRY(launch_status(frnn::launch_point_stats(d_pts, N, dim, e->stats_ws, s), "statistics launch"));
-    ST_TRY(mark(2));
-    // stage 2: grid frame of first-coordinate plans with D > g
+    ST_TRY(mark_stage(e, 2));
+    // stage 2: grid frame (projected, or raw)
     if (framed)
         ST_TRY(launch_status(frnn::launch_frame(d_pts, N, dim, plan, cells, e->stats_ws, e->frame_ws, s),
                              "frame launch"));
-    ST_TRY(mark(3));
+    ST_TRY(mark_stage(e, 3));
     // stage 3: bin + count (run_insert_points, frnn_engine.cu:159-160)
     if (grid)
         ST_TRY(launch_status(frnn::launch_bin_count(d_pts, N, plan.grid_dim, plan.res, plan.inv_cell, frame,
                                                     (int)cells, e->cell_of, e->rank, e->cnt, s),
                              "bin/count launch"));
-    ST_TRY(mark(4));
+    ST_TRY(mark_stage(e, 4));
     // stage 4: exclusive scan of the counts (thrust::exclusive_scan, frnn_engine.cu:91-94)
     if (grid)
         ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)cells + 1, e->start, e->partials, s),
                              "scan launch"));
-    ST_TRY(mark(5));
+    ST_TRY(mark_stage(e, 5));
     // stage 5: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
     // brute force, the AoS copy
     if (grid)
@@ -231,10 +247,51 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     else
         ST_TRY(launch_status(frnn::launch_transpose(d_pts, N, dim, e->aos, e->stats_ws, frows, s),
                              "transpose launch"));
-    // separate queries (part of stage 5): binned on the points' grid (the
-    // count array is free again after the scan), scanned and reordered into
-    // their own search order, or transposed for brute force; their filter
-    // rows are centred on the points' mean, as the points' are
+    b.valid = true;
+    return FRNN_OK;
+}
+
+// Stages 6-7 against a built grid: every point as a query (d_q == nullptr),
+// or the M queries d_q (SoA [d*M + j]), first binned on the points' grid and
+// reordered into their own search order (part of stage 5).
+int run_queries(frnn_engine* e, const BuiltGrid& b, const float* d_q, int M) {
+    const bool sep = d_q != nullptr;
+    const int Mq = sep ? M : b.N;   // queries = result rows
+    const int K = b.K;
+    e->has_result = false;
+    hipStream_t s = e->stream;
+    if (Mq == 0) {
+        e->has_result = true;
+        e->last_N = 0;
+        e->last_K = K;
+        return FRNN_OK;
+    }
+    if (b.plan.path == FRNN_PATH_EMPTY) {
+        // no points: every query row is padding (r2, -1)
+        ST_TRY(launch_status(frnn::launch_fill_i32(e->out_idx, (long long)Mq * K, -1, s), "padding"));
+        ST_TRY(launch_status(frnn::launch_fill_i32(reinterpret_cast<int*>(e->out_dist), (long long)Mq * K,
+                                                   (int)float_bits(b.ref_plan.r2), s),
+                             "padding"));
+        HIP_TRY(hipStreamSynchronize(s), "padding");
+        e->has_result = true;
+        e->last_N = Mq;
+        e->last_K = K;
+        return FRNN_OK;
+    }
+    const frnn_plan_t& plan = b.plan;
+    const int dim = b.dim, ds = b.ds, cap = b.cap;
+    const bool grid = b.grid;
+    const long long cells = b.cells;
+    const void* frame = b.frame;
+    float* const frows = b.frows;
+    ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)Mq * cap, "allocating candidate lists"));
+    if (e->counting)
+        ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * kCounterSlots, 0, s),
+                             "clearing counters"));
+    // separate queries: binned on the points' grid (the count array is free
+    // again after the points' scan), scanned and reordered into their own
+    // search order, or transposed for brute force; their filter rows are
+    // centred on the points' mean, as the points' are
     frnn::QuerySet qs{};
     if (sep) {
         ST_TRY(grow(&e->q_aos, &e->q_aos_bytes, (size_t)M * ds, "allocating query rows"));
@@ -265,19 +322,19 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
         }
         qs = frnn::QuerySet{e->q_aos, q_frows, grid ? e->q_sorted_idx : nullptr, grid ? e->q_cell_of : nullptr, M};
     }
-    ST_TRY(mark(6));
+    ST_TRY(mark_stage(e, 6));
     // stage 6: neighbour search
     ST_TRY(launch_status(frnn::launch_search(e->aos, frows, e->stats_ws, grid ? e->sorted_idx : nullptr,
                                              grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
-                                             N, dim, K, plan, e->lists, cap,
+                                             b.N, dim, K, plan, e->lists, cap,
                                              e->counting ? e->counters : nullptr, s, sep ? &qs : nullptr),
                          "search launch"));
-    ST_TRY(mark(7));
+    ST_TRY(mark_stage(e, 7));
     // stage 7: results to the original query order (ScatterToOrigKernel)
     const int* qinv = grid ? (sep ? e->q_inv : e->inv) : nullptr;
     ST_TRY(launch_status(frnn::launch_unpermute(e->lists, cap, qinv, Mq, K, e->out_idx, e->out_dist, s),
                          "unpermute launch"));
-    ST_TRY(mark(8));
+    ST_TRY(mark_stage(e, 8));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
     if (e->profiling)
         for (int i = 0; i < FRNN_NUM_STAGES; ++i)
@@ -293,6 +350,15 @@ int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, floa
     e->last_N = Mq;
     e->last_K = K;
     return FRNN_OK;
+}
+
+// The whole device pipeline: build the N points' grid, then search every
+// point (d_q == nullptr) or the M queries d_q against it.
+int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius,
+                 const float* d_q = nullptr, int M = 0) {
+    e->has_result = false;
+    ST_TRY(build_points(e, e->built, d_pts, N, dim, K, radius));
+    return run_queries(e, e->built, d_q, M);
 }
 
 }  // namespace
@@ -460,21 +526,31 @@ int frnn_engine_search_gpu_queries(frnn_engine_t* e, const float* d_pts, int N, 
     if (M < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "M must be >= 0");
     if (M > e->max_p) return fail(FRNN_ERR_CAPACITY, "M exceeds max_points");
     if ((!d_pts && N > 0) || (!d_queries && M > 0)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    if (N == 0 && M > 0) {
-        // no points: every query row is padding
-        frnn_plan_t p{};
-        p.r2 = radius * radius;
-        ST_TRY(launch_status(frnn::launch_fill_i32(e->out_idx, (long long)M * K, -1, e->stream), "padding"));
-        ST_TRY(launch_status(frnn::launch_fill_i32(reinterpret_cast<int*>(e->out_dist), (long long)M * K,
-                                                   (int)float_bits(p.r2), e->stream),
-                             "padding"));
-        HIP_TRY(hipStreamSynchronize(e->stream), "padding");
-        e->has_result = true;
-        e->last_N = M;
-        e->last_K = K;
-    } else {
-        ST_TRY(run_pipeline(e, d_pts, N, dim, K, radius, d_queries ? d_queries : d_pts, M));
-    }
+    ST_TRY(run_pipeline(e, d_pts, N, dim, K, radius, d_queries ? d_queries : d_pts, M));
+    if (d_idxs) *d_idxs = e->out_idx;
+    if (d_dists) *d_dists = e->out_dist;
+    return FRNN_OK;
+}
+
+int frnn_engine_build(frnn_engine_t* e, const float* d_pts, int N, int dim, int K, float radius) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    ST_TRY(frnn_validate(e->max_p, N, dim, K, radius));
+    if (!d_pts && N > 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device points");
+    e->has_result = false;
+    ST_TRY(build_points(e, e->built, d_pts, N, dim, K, radius));
+    // the points' data now live in the engine's own buffers
+    HIP_TRY(hipStreamSynchronize(e->stream), "grid build");
+    return FRNN_OK;
+}
+
+int frnn_engine_query(frnn_engine_t* e, const float* d_queries, int M, int** d_idxs, float** d_dists) {
+    if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
+    if (!e->built.valid) return fail(FRNN_ERR_STATE, "query called before a grid was built");
+    if (M < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "M must be >= 0");
+    if (M > e->max_p) return fail(FRNN_ERR_CAPACITY, "M exceeds max_points");
+    if (!d_queries && M > 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device queries");
+    e->last_plan = e->built.ref_plan;
+    ST_TRY(run_queries(e, e->built, d_queries ? d_queries : e->aos, M));
     if (d_idxs) *d_idxs = e->out_idx;
     if (d_dists) *d_dists = e->out_dist;
     return FRNN_OK;

@@ -106,6 +106,8 @@ def _load():
                                     ctypes.POINTER(vp)], i32),
         "frnn_engine_search_gpu_queries": ([vp, vp, i32, vp, i32, i32, i32, f32, ctypes.POINTER(vp),
                                             ctypes.POINTER(vp)], i32),
+        "frnn_engine_build": ([vp, vp, i32, i32, i32, f32], i32),
+        "frnn_engine_query": ([vp, vp, i32, ctypes.POINTER(vp), ctypes.POINTER(vp)], i32),
         "frnn_engine_search": ([vp, vp, i64, i32, f32, vp, vp], i32),
         "frnn_engine_get_results": ([vp, i32, i32, vp, vp], i32),
         "frnn_engine_set_stream": ([vp, vp], i32),
@@ -216,6 +218,20 @@ class FRNNEngine:
                                                       ctypes.c_void_p(int(queries_ptr)), int(M), int(dim),
                                                       int(K), float(radius), ctypes.byref(di), ctypes.byref(dd)),
                "search_gpu_queries")
+        return int(di.value or 0), int(dd.value or 0)
+
+    def build(self, points_ptr, N, dim, K, radius):
+        """Build the grid of N points (SoA fp32 device pointer p[d*N + i]) once,
+        for any number of query() calls with this K and radius."""
+        _check(_load().frnn_engine_build(self._handle(), ctypes.c_void_p(int(points_ptr)), int(N), int(dim),
+                                         int(K), float(radius)), "build")
+
+    def query(self, queries_ptr, M):
+        """Search M queries (SoA fp32 device pointer q[d*M + j]) against the last
+        built grid -> (d_idxs_ptr, d_dists_ptr), SoA [k*M + j]."""
+        di, dd = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(_load().frnn_engine_query(self._handle(), ctypes.c_void_p(int(queries_ptr)), int(M),
+                                         ctypes.byref(di), ctypes.byref(dd)), "query")
         return int(di.value or 0), int(dd.value or 0)
 
     def get_results(self, N, K):

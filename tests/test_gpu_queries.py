@@ -96,3 +96,42 @@ def test_metric_points_with_separate_queries_sampled():
     sel = np.sort(np.random.RandomState(3).choice(len(Q), 400, replace=False))
     ri, rd = O.search_queries(w.X, Q[sel], w.K, w.radius)
     assert_rows_equal(gi[sel], gd[sel], ri, rd, "metric queries sampled")
+
+
+@pytest.mark.parametrize("label,D,k,N,r,K,path", [c for c in CASES if c[0] in
+                                                  ("full_d3_rev", "first_d16", "full_d5", "bf_d16")])
+def test_grid_reuse_across_query_sets(label, D, k, N, r, K, path):
+    """build() once, then query() several query sets against the same grid;
+    the input points are overwritten after the build (the grid owns a copy)."""
+    X = unit_cloud(N, D, k, 11)
+    eng = frnn_cuda.FRNNEngine(max_points=2000)
+    dp = device_soa(X)
+    eng.build(dp.data_ptr(), N, D, K, r)
+    dp.fill_(float("nan"))
+    assert eng.last_plan()["path"] == path
+    for seed, M in ((5, 700), (6, 1), (7, 2000), (8, 0)):
+        Q = separate_queries(X, M, seed) if M > 1 else X[:M] + np.float32(0.001)
+        log(f"reuse {label}: query set M={M}")
+        dq = device_soa(Q) if M else device_soa(X[:1])
+        eng.query(dq.data_ptr(), M)
+        gi, gd = eng.get_results_numpy(M, K)
+        ri, rd = O.search_queries(X, Q, K, r)
+        assert_rows_equal(gi.reshape(K, M).T, gd.reshape(K, M).T, ri, rd, f"reuse {label} M={M}")
+    eng.close()
+
+
+def test_query_before_build_and_after_search():
+    X = unit_cloud(1500, 12, 3, 24)
+    eng = frnn_cuda.FRNNEngine(max_points=1500)
+    d = device_soa(X)
+    with pytest.raises(frnn_cuda.FRNNError, match="before a grid was built"):
+        eng.query(d.data_ptr(), 10)
+    # an all-points search leaves its grid for query() to reuse
+    eng.search_gpu(d.data_ptr(), 1500, 12, 16, 0.1)
+    Q = separate_queries(X, 300, 9)
+    dq = device_soa(Q)
+    eng.query(dq.data_ptr(), 300)
+    gi, gd = eng.get_results_numpy(300, 16)
+    ri, rd = O.search_queries(X, Q, 16, 0.1)
+    assert_rows_equal(gi.reshape(16, 300).T, gd.reshape(16, 300).T, ri, rd, "query after search_gpu")
+    eng.close()
