@@ -135,3 +135,21 @@ def test_query_before_build_and_after_search():
     ri, rd = O.search_queries(X, Q, 16, 0.1)
     assert_rows_equal(gi.reshape(16, 300).T, gd.reshape(16, 300).T, ri, rd, "query after search_gpu")
     eng.close()
+
+
+@pytest.mark.parametrize("name,M,nq", [("C2", 50_000, 600), ("C5", 3_000, 100)])
+def test_full_size_points_with_separate_queries(name, M, nq):
+    """Separate queries against full-size BASELINE point sets: the raw-frame
+    D=3 grid with the reversed distance order (C2) and D=128 brute force (C5);
+    sampled rows against the oracle over all points."""
+    w = W.config(name)
+    rs = np.random.RandomState(78)
+    spread = 0.3 * w.radius / np.sqrt(w.D)        # offsets of norm ~0.3 r
+    Q = (w.X[rs.randint(0, w.N, M)] + spread * rs.standard_normal((M, w.D))).astype(np.float32)
+    log(f"full-size {name}: N={w.N} points, M={M} separate queries")
+    gi, gd, plan = engine_search_queries(w.X, Q, w.K, w.radius)
+    assert plan["path"] == ("grid_full" if name == "C2" else "bruteforce")
+    sel = np.sort(rs.choice(M, nq, replace=False))
+    ri, rd = O.search_queries(w.X, Q[sel], w.K, w.radius)
+    assert_rows_equal(gi[sel], gd[sel], ri, rd, f"{name} separate queries sampled")
+    assert (gi[sel] >= 0).sum(1).mean() > 1
