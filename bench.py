@@ -98,6 +98,55 @@ def cpu_baseline(w, gi, gd, target_s, threads):
     }
 
 
+def bench_queries(args, w):
+    """Separate queries against a reused grid: the config's points are built
+    once (frnn_engine_build), then each timed step is one query() of M queries
+    (points near random points of the set, offsets of norm ~0.3 r)."""
+    import torch
+    import frnn_cuda
+    M = args.queries
+    rs = np.random.RandomState(78)
+    Q = (w.X[rs.randint(0, w.N, M)] + (0.3 * w.radius / np.sqrt(w.D)) * rs.standard_normal((M, w.D)))
+    Q = np.ascontiguousarray(Q.astype(np.float32).T)
+    dp = torch.from_numpy(w.soa()).to("cuda:0")
+    dq = torch.from_numpy(Q).to("cuda:0")
+    torch.cuda.synchronize()
+    eng = frnn_cuda.FRNNEngine(max_points=max(w.N, M))
+    builds = []
+    for _ in range(max(args.warmup // 4, 2)):
+        t0 = time.perf_counter()
+        eng.build(dp.data_ptr(), w.N, w.D, w.K, w.radius)
+        builds.append(time.perf_counter() - t0)
+    for _ in range(args.warmup):
+        eng.query(dq.data_ptr(), M)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.query(dq.data_ptr(), M)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    ms = 1e3 * float(np.mean(times))
+    eng.set_profiling(True, counters=True)
+    eng.query(dq.data_ptr(), M)
+    st = eng.stage_times()
+    ct = eng.counters()
+    plan = eng.last_plan()
+    eng.close()
+    print(json.dumps({
+        "metric": f"ms per query() call of {M} separate queries against a reused grid",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_median": round(1e3 * float(np.median(times)), 4), "higher_is_better": False,
+        "queries_per_s": round(M / (ms / 1e3), 1), "build_ms_median": round(1e3 * float(np.median(builds)), 4),
+        "dtype": "f32", "data": "synthetic (the config's points; queries near random points of the set)",
+        "config": {"workload": w.name, "N": w.N, "M": M, "D": w.D, "K": w.K, "radius": w.radius,
+                   "path": plan["path"]},
+        "search_kernel_ms": round(st["search"], 4),
+        "counters": {k: int(v) for k, v in ct.items()},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +157,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run three 256 MiB device copies (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--queries", type=int, default=0,
+                    help="instead of the all-points search: build the config's grid once and time "
+                         "query() calls of this many separate queries against it")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -133,6 +185,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     t_gen = time.perf_counter()
     w = W.config(args.config)
+    if args.queries > 0:
+        bench_queries(args, w)
+        return
     eprint(f"[bench] {w.name}: N={w.N} D={w.D} K={w.K} r={w.radius:.6f} "
            f"(data {time.perf_counter() - t_gen:.1f}s)")
     plan = frnn_cuda.plan(w.N, w.D, w.K, w.radius)

@@ -142,6 +142,7 @@ struct frnn_engine {
     bool profiling = false;   // per-stage HIP events
     bool counting = false;    // work counters (the counting search kernel)
     hipEvent_t ev[FRNN_NUM_STAGES + 1] = {};
+    bool ev_recorded[FRNN_NUM_STAGES + 1] = {};   // recorded since the last build
     float stage_ms[FRNN_NUM_STAGES] = {};
     long long ctr[FRNN_NUM_COUNTERS] = {};
     BuiltGrid built;          // the points' grid of the last build
@@ -169,7 +170,10 @@ void release(frnn_engine* e) {
 // Stage events: every call records the stages it runs; stage_times() reads
 // the ones of the last call that ran the search.
 int mark_stage(frnn_engine* e, int i) {
-    if (e->profiling) HIP_TRY(hipEventRecord(e->ev[i], e->stream), "event record");
+    if (e->profiling) {
+        HIP_TRY(hipEventRecord(e->ev[i], e->stream), "event record");
+        e->ev_recorded[i] = true;
+    }
     return FRNN_OK;
 }
 
@@ -177,6 +181,7 @@ int mark_stage(frnn_engine* e, int i) {
 // bin + count, scan, reorder (or the brute-force AoS copy).
 int build_points(frnn_engine* e, BuiltGrid& b, const float* d_pts, int N, int dim, int K, float radius) {
     b.valid = false;
+    for (bool& r : e->ev_recorded) r = false;
     ST_TRY(frnn_make_plan(N, dim, K, radius, &b.ref_plan));
     e->last_plan = b.ref_plan;
     // the grid the kernels bin and search on (the reference's, with a
@@ -337,8 +342,12 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, const float* d_q, int M) {
     ST_TRY(mark_stage(e, 8));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
     if (e->profiling)
-        for (int i = 0; i < FRNN_NUM_STAGES; ++i)
-            HIP_TRY(hipEventElapsedTime(&e->stage_ms[i], e->ev[i], e->ev[i + 1]), "event timing");
+        for (int i = 0; i < FRNN_NUM_STAGES; ++i) {
+            // stages the build ran without profiling read as 0
+            e->stage_ms[i] = 0.0f;
+            if (e->ev_recorded[i] && e->ev_recorded[i + 1])
+                HIP_TRY(hipEventElapsedTime(&e->stage_ms[i], e->ev[i], e->ev[i + 1]), "event timing");
+        }
     if (e->counting) {
         unsigned long long c[kCounterSlots];
         HIP_TRY(hipMemcpy(c, e->counters, sizeof(c), hipMemcpyDeviceToHost), "reading counters");

@@ -153,3 +153,23 @@ def test_full_size_points_with_separate_queries(name, M, nq):
     ri, rd = O.search_queries(w.X, Q[sel], w.K, w.radius)
     assert_rows_equal(gi[sel], gd[sel], ri, rd, f"{name} separate queries sampled")
     assert (gi[sel] >= 0).sum(1).mean() > 1
+
+
+def test_profiling_enabled_between_build_and_query():
+    # a build without profiling, then a profiled query: the build's stages
+    # read as 0, the query's search stage is timed, counters are kept
+    X = unit_cloud(3000, 16, 4, 25)
+    eng = frnn_cuda.FRNNEngine(max_points=3000)
+    d = device_soa(X)
+    eng.build(d.data_ptr(), 3000, 16, 32, 0.2)
+    eng.set_profiling(True, counters=True)
+    Q = separate_queries(X, 1000, 10)
+    dq = device_soa(Q)
+    eng.query(dq.data_ptr(), 1000)
+    st = eng.stage_times()
+    assert st["bin_count"] == 0 and st["search"] > 0 and st["unpermute"] > 0
+    assert eng.counters()["accepted"] > 0
+    gi, gd = eng.get_results_numpy(1000, 32)
+    ri, rd = O.search_queries(X, Q, 32, 0.2)
+    assert_rows_equal(gi.reshape(32, 1000).T, gd.reshape(32, 1000).T, ri, rd, "profiled query")
+    eng.close()
