@@ -256,11 +256,10 @@ int build_points(frnn_engine* e, BuiltGrid& b, const float* d_pts, int N, int di
     return FRNN_OK;
 }
 
-// Stages 6-7 against a built grid: every point as a query (d_q == nullptr),
-// or the M queries d_q (SoA [d*M + j]), first binned on the points' grid and
+// Stages 6-7 against a built grid: every point as a query (sep false), or
+// the M queries d_q (SoA [d*M + j]), first binned on the points' grid and
 // reordered into their own search order (part of stage 5).
-int run_queries(frnn_engine* e, const BuiltGrid& b, const float* d_q, int M) {
-    const bool sep = d_q != nullptr;
+int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, int M) {
     const int Mq = sep ? M : b.N;   // queries = result rows
     const int K = b.K;
     e->has_result = false;
@@ -362,12 +361,12 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, const float* d_q, int M) {
 }
 
 // The whole device pipeline: build the N points' grid, then search every
-// point (d_q == nullptr) or the M queries d_q against it.
-int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius,
+// point (sep false) or the M queries d_q against it.
+int run_pipeline(frnn_engine* e, const float* d_pts, int N, int dim, int K, float radius, bool sep = false,
                  const float* d_q = nullptr, int M = 0) {
     e->has_result = false;
     ST_TRY(build_points(e, e->built, d_pts, N, dim, K, radius));
-    return run_queries(e, e->built, d_q, M);
+    return run_queries(e, e->built, sep, d_q, M);
 }
 
 }  // namespace
@@ -535,7 +534,7 @@ int frnn_engine_search_gpu_queries(frnn_engine_t* e, const float* d_pts, int N, 
     if (M < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "M must be >= 0");
     if (M > e->max_p) return fail(FRNN_ERR_CAPACITY, "M exceeds max_points");
     if ((!d_pts && N > 0) || (!d_queries && M > 0)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
-    ST_TRY(run_pipeline(e, d_pts, N, dim, K, radius, d_queries ? d_queries : d_pts, M));
+    ST_TRY(run_pipeline(e, d_pts, N, dim, K, radius, true, d_queries, M));
     if (d_idxs) *d_idxs = e->out_idx;
     if (d_dists) *d_dists = e->out_dist;
     return FRNN_OK;
@@ -559,7 +558,7 @@ int frnn_engine_query(frnn_engine_t* e, const float* d_queries, int M, int** d_i
     if (M > e->max_p) return fail(FRNN_ERR_CAPACITY, "M exceeds max_points");
     if (!d_queries && M > 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device queries");
     e->last_plan = e->built.ref_plan;
-    ST_TRY(run_queries(e, e->built, d_queries ? d_queries : e->aos, M));
+    ST_TRY(run_queries(e, e->built, true, d_queries, M));
     if (d_idxs) *d_idxs = e->out_idx;
     if (d_dists) *d_dists = e->out_dist;
     return FRNN_OK;

@@ -73,9 +73,18 @@ def test_empty_query_and_point_sets():
     X = unit_cloud(500, 3, 3, 23)
     eng = frnn_cuda.FRNNEngine(max_points=500)
     dp = device_soa(X)
-    # no queries: nothing to return
+    # no queries (also with a null query pointer): nothing to return, and no
+    # all-points search in their place
     eng.search_gpu_queries(dp.data_ptr(), 500, dp.data_ptr(), 0, 3, 8, 0.1)
     assert eng.get_results_numpy(0, 8)[0].size == 0
+    Q = separate_queries(X, 500, 11)
+    dq = device_soa(Q)
+    eng.search_gpu_queries(dp.data_ptr(), 500, dq.data_ptr(), 500, 3, 8, 0.1)
+    before = eng.get_results_numpy(500, 8)
+    eng.search_gpu_queries(dp.data_ptr(), 500, 0, 0, 3, 8, 0.1)
+    eng.query(0, 0)
+    after = eng.get_results_numpy(500, 8)          # the output buffers, untouched
+    assert np.array_equal(before[0], after[0]) and np.array_equal(before[1], after[1])
     # no points: every query row is padding (r2, -1)
     eng.search_gpu_queries(dp.data_ptr(), 0, dp.data_ptr(), 500, 3, 8, 0.1)
     idx, dist = eng.get_results_numpy(500, 8)
