@@ -279,16 +279,38 @@ int frnn_uses_filter_rows(int dim);
  * cell-sorted AoS points, d_sorted_idx, d_cell_of (cell id per original
  * point), d_start (frnn_grid_cells + 1 exclusive offsets) and, for
  * first-coordinate plans, the frame workspace; brute force reads the
- * transposed AoS points and ignores them.  Results: for sorted position s,
- * entries d_lists[s*list_cap + k], k < K, hold ascending keys
+ * transposed AoS points and ignores them.
+ *
+ * queries == NULL: every point is a query (the engine's all-points search,
+ * run_find_nbrs(d_points, d_points, ...) as frnn_engine.cu:241-245 calls it).
+ * Otherwise the M queries of *queries are searched against the N points: the
+ * two-array form run_find_nbrs(d_points1 = queries, d_points2 = points, ...)
+ * (find_nbrs.cu:562-567; run_find_nbrs_griddim :597-633) and
+ * run_bruteforce(d_p1, d_p2, P1, P2, ...) (no_grid_frnn.cu:273-276).
+ *
+ * Results: for search position s (sorted position of the point, or of the
+ * query), entries d_lists[s*list_cap + k], k < K, hold ascending keys
  * (bits(d2) << 32 | idx) with padding (bits(r2) << 32 | 0xffffffff).
- * d_counters (5 u64: the FRNN_NUM_COUNTERS work counters and a capacity-guard
- * counter; may be NULL) accumulates the counters. */
+ * list_cap >= K; below frnn_list_capacity(K) a list can overflow, and then
+ * *d_status (a device-visible word the caller zeroes; may be NULL) is set to 1
+ * and the lists are not valid.  d_counters (5 u64: the FRNN_NUM_COUNTERS work
+ * counters and a capacity-guard counter; may be NULL) runs the counting build
+ * of the kernel and accumulates the counters. */
+typedef struct frnn_queries {
+    int M;                      /* number of queries */
+    const float* d_aos;         /* [M x frnn_aos_stride(dim)] rows in search order: frnn_launch_reorder
+                                   of the queries binned on the points' grid, or frnn_launch_transpose
+                                   for brute force */
+    const float* d_frows;       /* their centred rows (when frnn_uses_filter_rows(dim)), centred on the
+                                   points' statistics */
+    const int* d_sorted_idx;    /* search position -> original query index (grid paths) */
+    const int* d_cell_of;       /* original query index -> cell id on the points' grid (grid paths) */
+} frnn_queries_t;
 int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const void* d_stats_ws,
                           const int* d_sorted_idx, const int* d_cell_of, const int* d_start,
                           const void* d_frame_ws, int N, int dim, int K, const frnn_plan_t* plan,
-                          unsigned long long* d_lists, int list_cap,
-                          unsigned long long* d_counters, void* stream);
+                          const frnn_queries_t* queries, unsigned long long* d_lists, int list_cap,
+                          unsigned long long* d_counters, unsigned int* d_status, void* stream);
 
 /* run_scatter_to_orig (find_nbrs.cu:505-535): output row of original query i is
  * list row d_inv[i] (identity when d_inv is NULL); writes SoA [k*N+i]. */

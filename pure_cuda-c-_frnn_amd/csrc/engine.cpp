@@ -109,6 +109,11 @@ struct frnn_engine {
     int* start = nullptr;
     int* partials = nullptr;
     unsigned long long* counters = nullptr;
+    // status word of the search kernel's capacity guards, in pinned host
+    // memory (the kernel writes it only when a guard fires; read after the
+    // call's stream synchronisation, no copy)
+    unsigned* status_host = nullptr;
+    unsigned* status_dev = nullptr;
     int* out_idx = nullptr;
     float* out_dist = nullptr;
     float* aos = nullptr;
@@ -163,6 +168,7 @@ void release(frnn_engine* e) {
                     e->q_inv, e->q_start, e->q_aos, e->q_frows};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    if (e->status_host) (void)hipHostFree(e->status_host);
     for (auto& ev : e->ev)
         if (ev) (void)hipEventDestroy(ev);
 }
@@ -328,10 +334,12 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
     }
     ST_TRY(mark_stage(e, 6));
     // stage 6: neighbour search
+    __atomic_store_n(e->status_host, 0u, __ATOMIC_SEQ_CST);
     ST_TRY(launch_status(frnn::launch_search(e->aos, frows, e->stats_ws, grid ? e->sorted_idx : nullptr,
                                              grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
                                              b.N, dim, K, plan, e->lists, cap,
-                                             e->counting ? e->counters : nullptr, s, sep ? &qs : nullptr),
+                                             e->counting ? e->counters : nullptr, e->status_dev, s,
+                                             sep ? &qs : nullptr),
                          "search launch"));
     ST_TRY(mark_stage(e, 7));
     // stage 7: results to the original query order (ScatterToOrigKernel)
@@ -340,6 +348,8 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
                          "unpermute launch"));
     ST_TRY(mark_stage(e, 8));
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
+    if (__atomic_load_n(e->status_host, __ATOMIC_SEQ_CST) != 0)
+        return fail(FRNN_ERR_HIP, "internal list/queue capacity overflow in the search kernel");
     if (e->profiling)
         for (int i = 0; i < FRNN_NUM_STAGES; ++i) {
             // stages the build ran without profiling read as 0
@@ -480,6 +490,9 @@ int frnn_engine_create(int max_points, frnn_engine_t** out) {
     alloc((void**)&e->start, C * sizeof(int));
     alloc((void**)&e->partials, (size_t)frnn::scan_partials_count((int)C) * sizeof(int));
     alloc((void**)&e->counters, kCounterSlots * sizeof(unsigned long long));
+    if (err == hipSuccess) err = hipHostMalloc((void**)&e->status_host, 64, hipHostMallocDefault);
+    if (err == hipSuccess) err = hipHostGetDevicePointer((void**)&e->status_dev, e->status_host, 0);
+    if (err == hipSuccess) *e->status_host = 0u;
     // engine-owned outputs sized max_points*128 as the reference (frnn_engine.cu:39-40)
     alloc((void**)&e->out_idx, P * FRNN_MAX_K * sizeof(int));
     alloc((void**)&e->out_dist, P * FRNN_MAX_K * sizeof(float));
@@ -739,17 +752,21 @@ int frnn_launch_transpose(const float* d_pts, int N, int dim, float* d_aos, cons
 int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const void* d_stats_ws,
                           const int* d_sorted_idx, const int* d_cell_of, const int* d_start,
                           const void* d_frame_ws, int N, int dim, int K, const frnn_plan_t* plan,
-                          unsigned long long* d_lists, int list_cap, unsigned long long* d_counters,
-                          void* stream) {
+                          const frnn_queries_t* queries, unsigned long long* d_lists, int list_cap,
+                          unsigned long long* d_counters, unsigned int* d_status, void* stream) {
     if (!plan) return fail(FRNN_ERR_INVALID_ARGUMENT, "null plan");
     ST_TRY(frnn_validate(0, N, dim, K, plan->cell_size));
-    if (plan->path == FRNN_PATH_EMPTY || N == 0) return FRNN_OK;
-    if (list_cap < frnn::list_capacity(K)) return fail(FRNN_ERR_INVALID_ARGUMENT, "list_cap too small");
+    if (queries && queries->M < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "queries->M must be >= 0");
+    if (plan->path == FRNN_PATH_EMPTY || N == 0 || (queries && queries->M == 0)) return FRNN_OK;
+    if (list_cap < K) return fail(FRNN_ERR_INVALID_ARGUMENT, "list_cap must be >= K");
     const bool grid = plan->path != FRNN_PATH_BRUTEFORCE;
     if (!d_aos || !d_stats_ws || !d_lists || (grid && (!d_sorted_idx || !d_cell_of || !d_start)))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
     if (frnn::uses_filter_rows(dim) && !d_frows)
         return fail(FRNN_ERR_INVALID_ARGUMENT, "this dimension needs the centred filter rows");
+    if (queries && (!queries->d_aos || (grid && (!queries->d_sorted_idx || !queries->d_cell_of)) ||
+                    (frnn::uses_filter_rows(dim) && !queries->d_frows)))
+        return fail(FRNN_ERR_INVALID_ARGUMENT, "null query pointer");
     if (grid && (plan->grid_dim < 1 || plan->grid_dim > 9 || plan->grid_dim > dim || plan->res < 1 ||
                  ipow_sat(plan->res, plan->grid_dim, (long long)4e18) != plan->cells ||
                  plan->cells > FRNN_MAX_CELLS))
@@ -757,9 +774,13 @@ int frnn_launch_find_nbrs(const float* d_aos, const float* d_frows, const void* 
     if (plan->rev_order && (!grid || dim != 3)) return fail(FRNN_ERR_INVALID_ARGUMENT, "reversed order is D=3 grid only");
     if (d_frame_ws && !frnn::has_frame(*plan, dim))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "a frame given for a plan without one");
+    frnn::QuerySet qs{};
+    if (queries)
+        qs = frnn::QuerySet{queries->d_aos, queries->d_frows, grid ? queries->d_sorted_idx : nullptr,
+                            grid ? queries->d_cell_of : nullptr, queries->M};
     return launch_status(frnn::launch_search(d_aos, d_frows, d_stats_ws, d_sorted_idx, d_cell_of, d_start,
                                              d_frame_ws, N, dim, K, *plan, d_lists, list_cap, d_counters,
-                                             (hipStream_t)stream),
+                                             d_status, (hipStream_t)stream, queries ? &qs : nullptr),
                          "search launch");
 }
 

@@ -14,13 +14,13 @@ __host__ __device__ inline int aos_stride(int D) {
     return D <= 4 ? 4 : D <= 8 ? 8 : D <= 12 ? 12 : D <= 16 ? 16 : D <= 32 ? 32 : D <= 64 ? 64 : 128;
 }
 
-// Per-query candidate list entries: K kept after a compaction, room for a full
-// 64-entry recheck batch and at least 32 more arrivals between compactions; at
-// least 160 (a compaction once a list holds more than 96 keys), which measured
-// fastest at K = 32 and 64: earlier compactions tighten the query's threshold
-// sooner, later ones sort less often.  At most 256, the largest register
-// sort of the search kernel.
-inline int list_capacity(int K) { return K + 96 > 160 ? K + 96 : 160; }
+// Per-query candidate list entries: 256 for every K.  The search keeps a
+// histogram of each list's keys by distance and lowers the query's threshold
+// as soon as K keys lie below a bucket edge, so a list fills up slowly; with
+// 255 usable entries most lists never need a compaction before the final
+// selection (a sort of at most 128 keys after dropping the keys above the
+// threshold).
+inline int list_capacity(int /*K*/) { return 256; }
 
 int scan_partials_count(int n);
 
@@ -160,7 +160,7 @@ struct QuerySet {
 int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
                   const int* cell_of,
                   const int* start, const void* frame_ws, int N, int D, int K, const frnn_plan_t& plan,
-                  unsigned long long* lists, int cap, unsigned long long* counters, hipStream_t s,
-                  const QuerySet* queries = nullptr);
+                  unsigned long long* lists, int cap, unsigned long long* counters, unsigned* status,
+                  hipStream_t s, const QuerySet* queries = nullptr);
 
 }  // namespace frnn

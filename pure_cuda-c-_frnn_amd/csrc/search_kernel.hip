@@ -28,10 +28,13 @@
 //     (d2, idx) keys go to a per-query candidate list.  Every pair within the
 //     radius lies in the query's shell, so candidates streamed for other
 //     queries of the wave need no membership test: they fail the exact test;
-//   * when a list nears capacity the wave sorts it cooperatively (bitonic in
-//     registers, up to 4 keys per lane), keeps the K smallest and tightens the
-//     query's threshold to the K-th key; at the end every list is sorted and its
-//     first K keys (plus padding) are the result for that sorted position.
+//   * every query keeps a histogram of its list's keys by distance; as soon as
+//     K keys lie below a bucket edge its threshold drops to that edge.  A list
+//     that nears capacity first drops its keys above the threshold; if it is
+//     still long, the wave sorts it cooperatively (bitonic in registers, up to
+//     4 keys per lane), keeps the K smallest and tightens the threshold to the
+//     K-th key; at the end every list is sorted and its first K keys (plus
+//     padding) are the result for that sorted position.
 //
 // Exactness: a pair is returned iff its exact fp32 distance in the reference
 // order is < r2 and it is among the K smallest (d2, idx) keys.  The MFMA value
@@ -40,6 +43,8 @@
 // fp32 MFMA accumulation (with a factor 2 on the unit roundoff) and the exact
 // order, so no pair that could qualify is dropped.  NaN or overflowed filter
 // values are always re-evaluated.
+#include <cstring>
+
 #include "frnn_device.hpp"
 #include "frnn_internal.hpp"
 
@@ -63,6 +68,31 @@ __device__ __forceinline__ void lds_sync() {
 }
 constexpr int kRing = 128;                   // pending candidate runs (<= 31 + 64 in use)
 constexpr int kMaxG = 9;
+
+// Threshold histograms.  Each query counts the keys of its list by bucket of
+// their squared distance below r2.  Non-negative fp32 bit patterns order like
+// the values, so with top = bits(r2) and d2 < r2
+//   bucket(d2) = B - 1 - min((top - 1 - bits(d2)) >> S, B - 1):
+// bucket b >= 1 holds the bit patterns [top - (B-b) 2^S, top - (B-1-b) 2^S),
+// bucket 0 everything below its upper edge top - (B-1) 2^S.  Once the buckets
+// up to b hold at least K keys of the list, the K-th smallest key lies below
+// bucket b's upper edge, so no key at or above it can be among the K results:
+// the query's threshold drops to that edge without sorting the list.  Buckets
+// are a quarter octave of d2 wide (S = 21) and reach 4 octaves below r2.
+// Counts are bytes, four to a word (a list never holds more than 255 keys).
+constexpr int kHB = 16;                      // buckets per query
+constexpr int kHS = 21;                      // bucket width: 2^21 fp32 ulps of d2
+constexpr int kHW = kHB / 4;                 // histogram words per query
+constexpr int kMaxRoom = 255;                // list entries in use (byte counts)
+
+__device__ __forceinline__ int hist_bucket(float d2, unsigned top) {
+    const unsigned u = (top - 1u - __float_as_uint(d2)) >> kHS;
+    return kHB - 1 - (int)min(u, (unsigned)(kHB - 1));
+}
+// key just above bucket b: a key is below it iff its d2 lies in a bucket <= b
+__device__ __forceinline__ unsigned long long hist_edge_key(int b, unsigned top) {
+    return (unsigned long long)(top - ((unsigned)(kHB - 1 - b) << kHS)) << 32;
+}
 
 // Traversal order of a segment's 3^m neighbouring rows (m = g - 1 axes): by
 // the number of axes on which the row is offset (the segment's own row, then
@@ -119,9 +149,13 @@ struct SearchArgs {
     const int* qcell_of;
     unsigned long long* lists;   // [M][cap] candidate keys
     unsigned long long* counters;
+    unsigned* status;            // set to 1 if a capacity guard fired (may be null)
     int N, M, D, K, cap, G, res; // N points, M queries; res: raw-grid cells per axis
     int gstride[kMaxG];          // raw-grid cell-id stride per axis
-    int room;                    // usable list entries: min(cap, largest register sort)
+    int room;                    // usable list entries: min(cap, kMaxRoom)
+    int hist_on;                 // threshold histograms in use (r2 is not tiny)
+    int exact_limit;             // a filtered list above this gets the exact compaction
+    unsigned r2bits;             // bits(r2)
     float r2, cell, radius;      // cell: raw-grid cell edge
     float norm_scale;            // 1 - c_norm
     float thr_rel, thr_abs;      // filter threshold margin
@@ -196,6 +230,14 @@ void search_kernel(SearchArgs a) {
     __shared__ int s_cnt[kQB];
     __shared__ int s_srt[kQB];       // sorted prefix length of each list
     __shared__ unsigned long long s_thr[kQB];
+    // threshold histograms: byte b of query n's words is its bucket b count;
+    // s_hb[n], the lowest bucket whose keys and those below number at least K
+    // once that happens (B - 1 before); s_hcle[n], the number of keys in
+    // buckets <= s_hb[n].  Every accepted key is below the threshold, which
+    // never exceeds bucket s_hb[n]'s upper edge, so it lands in such a bucket.
+    __shared__ unsigned s_hist[kQB * kHW];
+    __shared__ int s_hcle[kQB];
+    __shared__ unsigned char s_hb[kQB];
     __shared__ unsigned long long s_ctr[5];
     // Rows of up to 32 floats re-evaluate a tile's hits right after its MFMA
     // chain, from the tile's raw rows staged in LDS; wider rows queue hits as
@@ -204,8 +246,11 @@ void search_kernel(SearchArgs a) {
     __shared__ unsigned char s_qn[kTileExact ? 1 : kQueueCap];
     __shared__ int s_qpos[kTileExact ? 1 : kQueueCap];
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points
-    // at virtual stream positions [vbeg, vend)
-    __shared__ int r_start[kRing], r_vbeg[kRing], r_vend[kRing];
+    // at virtual stream positions [vbeg, vend).  Runs are contiguous in the
+    // stream, so a run's vbeg is the vend of the run before it (slot
+    // kRing - 1 starts at 0 for the first run; at most 96 slots are in use,
+    // so the slot before a pending run is never overwritten).
+    __shared__ int r_start[kRing], r_vend[kRing];
     // current tile, per candidate row: the sorted position (queue path) or
     // the original index and the raw row (tile-exact path), and the hit
     // entries (row << 5 | query).  Staged rows are TS floats apart: RS as s_q, except
@@ -261,7 +306,12 @@ void search_kernel(SearchArgs a) {
         s_cnt[lane] = 0;
         s_srt[lane] = 0;
         s_thr[lane] = make_key(a.r2, 0);
+        s_hcle[lane] = 0;
+        s_hb[lane] = (unsigned char)(kHB - 1);
     }
+#pragma unroll
+    for (int i = lane; i < kQB * kHW; i += kWave) s_hist[i] = 0u;
+    if (lane == 0) r_vend[kRing - 1] = 0;
     lds_sync();
     // Filter operands are the rows centred on the input mean, fl(x - mean).
     // Rows of up to 32 floats are centred in registers as they are loaded
@@ -320,7 +370,69 @@ void search_kernel(SearchArgs a) {
     auto bump = [&](int i, unsigned long long v) __attribute__((always_inline)) {
         if (counting && lane == 0) s_ctr[i] += v;
     };
+    // A capacity guard fired (a logic error): the caller's status word says so
+    // (wave-uniform call).
+    auto report_overflow = [&](bool ovf) __attribute__((always_inline)) {
+        if (counting) bump(4, __popcll(__ballot(ovf)));
+        if (a.status && __ballot(ovf) != 0 && lane == 0) a.status[0] = 1u;
+    };
     int q_size = 0;                     // queue entries (wave-uniform)
+
+    // An exactly re-evaluated key below query qn's threshold joins its list.
+    auto accept = [&](int qn, unsigned long long key, bool& ovf) __attribute__((always_inline)) {
+        const int slot = atomicAdd(&s_cnt[qn], 1);
+        // compaction before each round leaves >= kBatch free slots; the guard
+        // only keeps a logic error (or a caller's too-small list) from writing
+        // past the list
+        if (slot < a.room) lists[(size_t)qn * a.cap + slot] = key;
+        else ovf = true;
+    };
+    // End of a round (wave-uniform call; acc: this lane accepted `key` for
+    // query qn).  The accepted keys join their queries' histograms; then every
+    // query whose buckets up to a lower one now hold >= K keys moves s_hb down
+    // and its threshold to that bucket's upper edge.  Only query n's own lanes
+    // use its threshold before the next barrier (the hit tests of the next
+    // tile), so they take it into thr_f directly; other lanes read s_thr after
+    // the barrier that starts the next staging or round.  (The histogram
+    // update waits for the round's end, when the rows of the exact evaluation
+    // are no longer live.)
+    auto end_round = [&](bool acc, int qn, unsigned long long key) __attribute__((always_inline)) {
+        const bool any = __ballot(acc) != 0;
+        if (a.hist_on && any && acc) {
+            const int b = hist_bucket(key_d2(key), a.r2bits);
+            atomicAdd(&s_hist[qn * kHW + (b >> 2)], 1u << (8 * (b & 3)));
+            atomicAdd(&s_hcle[qn], 1);
+        }
+        lds_sync();
+        if (a.hist_on && any && qvalid) {
+            int cle = s_hcle[n];
+            if (cle >= a.K) {
+                const unsigned char* hb = reinterpret_cast<const unsigned char*>(s_hist) + n * kHB;
+                const int b0 = s_hb[n];
+                int b = b0;
+                int cb = hb[b];
+                while (b > 0 && cle - cb >= a.K) {
+                    cle -= cb;
+                    --b;
+                    cb = hb[b];
+                }
+                if (b != b0) {
+                    const unsigned long long ek = hist_edge_key(b, a.r2bits);
+                    const unsigned long long t = s_thr[n];
+                    const unsigned long long nt = ek < t ? ek : t;
+                    thr_f = filter_threshold(key_d2(nt), a);
+                    if (h == 0) {
+                        s_hb[n] = (unsigned char)b;
+                        s_hcle[n] = cle;
+                        s_thr[n] = nt;
+                    }
+                }
+            }
+        }
+        // one wave: its LDS accesses execute in program order; the fence keeps
+        // the compiler from moving later reads of s_thr above these writes
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local");
+    };
 
     // Selection on query qn's candidate list.  A list keeps its first s_srt[qn]
     // keys sorted (the K kept at the last compaction); later arrivals follow
@@ -381,9 +493,10 @@ void search_kernel(SearchArgs a) {
                 const int i = e * kWave + lane;
                 if (i < keep) L[i] = x[e];
             }
+            unsigned long long kth = 0;
             if (c >= a.K) {
                 const int ek = (a.K - 1) / kWave;
-                unsigned long long kth = x[0];
+                kth = x[0];
 #pragma unroll
                 for (int e = 1; e < EK; ++e)
                     if (e == ek) kth = x[e];
@@ -394,11 +507,64 @@ void search_kernel(SearchArgs a) {
                 s_cnt[qn] = keep;
                 s_srt[qn] = keep;
             }
+            if (a.hist_on) {
+                // the list now holds the `keep` smallest keys: rebuild its
+                // histogram from them (every kept key is <= the K-th, so in a
+                // bucket <= the K-th key's)
+                if (lane < kHW) s_hist[qn * kHW + lane] = 0u;
+                lds_sync();
+#pragma unroll
+                for (int e = 0; e < EK; ++e) {
+                    const int i = e * kWave + lane;
+                    if (i < keep) {
+                        const int b = hist_bucket(key_d2(x[e]), a.r2bits);
+                        atomicAdd(&s_hist[qn * kHW + (b >> 2)], 1u << (8 * (b & 3)));
+                    }
+                }
+                if (lane == 0) {
+                    s_hcle[qn] = keep;
+                    s_hb[qn] = (unsigned char)(c >= a.K ? hist_bucket(key_d2(kth), a.r2bits) : kHB - 1);
+                }
+            }
         }
         lds_sync();
     };
+    // Filter compaction of query qn's list: drop the keys above its threshold
+    // (they can no longer be among the K results), keeping the order, so the
+    // sorted prefix stays sorted.  Every key counted in the histogram's
+    // buckets <= s_hb[qn] is <= the threshold and stays.  Returns the new length.
+    auto filter_list = [&](int qn) __attribute__((always_inline)) -> int {
+        unsigned long long* L = lists + (size_t)qn * a.cap;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        const int c = min(s_cnt[qn], a.room);
+        const int m = s_srt[qn];
+        const unsigned long long thr = s_thr[qn];
+        // chunk by chunk: the kept keys of chunks <= e move to positions below
+        // (e + 1) * 64, so no store reaches a chunk not yet loaded
+        int base = 0, nm = 0;
+        for (int e = 0; e * kWave < c; ++e) {
+            const int i = e * kWave + lane;
+            const unsigned long long v = (i < c) ? L[i] : ~0ull;
+            const bool kp = i < c && v <= thr;
+            const unsigned long long mk = __ballot(kp);
+            const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(mk >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((unsigned)mk, 0u));
+            if (kp) L[pos] = v;
+            nm += __popcll(__ballot(kp && i < m));
+            base += __popcll(mk);
+        }
+        if (lane == 0) {
+            s_cnt[qn] = base;
+            s_srt[qn] = nm;
+        }
+        lds_sync();
+        return base;
+    };
     auto select_topk = [&](int qn, bool final_pass) __attribute__((always_inline)) {
-        const int c = s_cnt[qn];
+        // a final list with stale keys beyond two sort registers is filtered
+        // first (a smaller sort)
+        if (final_pass && a.hist_on && min(s_cnt[qn], a.room) - s_srt[qn] > 2 * kWave) filter_list(qn);
+        const int c = min(s_cnt[qn], a.room);
         const int m = s_srt[qn];
         const int nn = c - m;
         if (a.K <= kWave) {
@@ -411,42 +577,59 @@ void search_kernel(SearchArgs a) {
             else select_merge(IntC<2>{}, IntC<4>{}, qn, c, m, final_pass);
         }
     };
+    // Room for a round in query qn's list: first the filter compaction; if
+    // the list is still long (keys crowded into one bucket, or histograms
+    // off), the exact one, which keeps the K smallest.
+    auto compact = [&](int qn) __attribute__((always_inline)) {
+        if (a.hist_on && filter_list(qn) <= a.exact_limit) return;
+        select_topk(qn, false);
+    };
+    // Before a round: compact every list that could overflow during it, then
+    // reload the filter thresholds.
+    auto make_room = [&]() __attribute__((always_inline)) {
+        const bool need = (lane < kQB) && s_cnt[lane] > a.room - kBatch;
+        unsigned long long m = __ballot(need);
+        if (m) {
+            while (m) {
+                const int qn = __ffsll((long long)m) - 1;
+                m &= m - 1;
+                compact(qn);
+            }
+            if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
+        }
+    };
 
     // Exact re-evaluation of queue entries [base, base + count) (queue path).
     // First every list that could overflow during the batch is compacted; with
     // final_pass every list of the chunk gets its final selection instead.
     auto process_batch = [&](int base, int count, bool final_pass) __attribute__((always_inline)) {
+        // (one call site of the selection for both uses keeps a single
+        // inlined copy of the sorts)
         const bool need = (lane < kQB) && (final_pass ? lane < nq : s_cnt[lane] > a.room - kBatch);
         unsigned long long m = __ballot(need);
         if (m) {
             while (m) {
                 const int qn = __ffsll((long long)m) - 1;
                 m &= m - 1;
-                select_topk(qn, final_pass);
+                if (final_pass || !(a.hist_on && filter_list(qn) <= a.exact_limit)) select_topk(qn, final_pass);
             }
             if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
         }
         bool accepted = false, ovf = false;
+        int qn = 0;
+        unsigned long long key = 0;
         if (!kTileExact && lane < count) {
-            const int qn = s_qn[base + lane];
+            qn = s_qn[base + lane];
             const int pos = s_qpos[base + lane];
             const float e = exact_d2<DS, REV>(query_row(qn), a.pts + (size_t)pos * DS);
             const int idx = BF ? pos : a.sorted_idx[pos];
-            const unsigned long long key = make_key(e, idx);
+            key = make_key(e, idx);
             accepted = key < s_thr[qn];
-            if (accepted) {
-                const int slot = atomicAdd(&s_cnt[qn], 1);
-                // compaction above leaves >= kBatch free slots; the guard only
-                // keeps a logic error from writing past the list
-                if (slot < a.room) lists[(size_t)qn * a.cap + slot] = key;
-                else ovf = true;
-            }
+            if (accepted) accept(qn, key, ovf);
         }
-        if constexpr (counting) {
-            bump(2, __popcll(__ballot(accepted)));
-            bump(4, __popcll(__ballot(ovf)));
-        }
-        lds_sync();
+        if constexpr (counting) bump(2, __popcll(__ballot(accepted)));
+        report_overflow(ovf);
+        end_round(accepted, qn, key);
         q_size = base;
     };
 
@@ -478,7 +661,7 @@ void search_kernel(SearchArgs a) {
             if (jr < ring_tail) jr = ring_tail;
             while (r_vend[jr & (kRing - 1)] <= v) ++jr;
             const int j = jr & (kRing - 1);
-            t.pos = r_start[j] + (v - r_vbeg[j]);
+            t.pos = r_start[j] + (v - r_vend[(jr - 1) & (kRing - 1)]);
             if constexpr (kTileExact) {
                 // both halves of the wave load it (the same address: one
                 // coalesced access, and no per-half exec mask in the tile loop)
@@ -604,37 +787,22 @@ void search_kernel(SearchArgs a) {
         if (total == 0) return;
         lds_sync();
         for (int base = 0; base < total; base += kWave) {
-            const bool need = (lane < kQB) && s_cnt[lane] > a.room - kBatch;
-            unsigned long long m = __ballot(need);
-            if (m) {
-                while (m) {
-                    const int qn = __ffsll((long long)m) - 1;
-                    m &= m - 1;
-                    select_topk(qn, false);
-                }
-                if (qvalid) thr_f = filter_threshold(key_d2(s_thr[n]), a);
-            }
+            make_room();
             bool accepted = false, ovf = false;
+            int qn = 0;
+            unsigned long long key = 0;
             if (base + lane < total) {
                 const int e = s_hit[base + lane];
-                const int qn = e & 31;
+                qn = e & 31;
                 const int row = e >> 5;
                 const float d2 = exact_d2<DS, REV>(s_q + qn * RS, t_rows + row * TS);
-                const unsigned long long key = make_key(d2, t_idx[row]);
+                key = make_key(d2, t_idx[row]);
                 accepted = key < s_thr[qn];
-                if (accepted) {
-                    const int slot = atomicAdd(&s_cnt[qn], 1);
-                    // compaction above leaves >= kBatch free slots; the guard
-                    // only keeps a logic error from writing past the list
-                    if (slot < a.room) lists[(size_t)qn * a.cap + slot] = key;
-                    else ovf = true;
-                }
+                if (accepted) accept(qn, key, ovf);
             }
-            if constexpr (counting) {
-                bump(2, __popcll(__ballot(accepted)));
-                bump(4, __popcll(__ballot(ovf)));
-            }
-            lds_sync();
+            if constexpr (counting) bump(2, __popcll(__ballot(accepted)));
+            report_overflow(ovf);
+            end_round(accepted, qn, key);
         }
     };
 
@@ -689,6 +857,7 @@ void search_kernel(SearchArgs a) {
                 }
             }
         }
+        if (q_size > kQueueCap && a.status && lane == 0) a.status[0] = 1u;
         lds_sync();
         int qs = min(q_size, kQueueCap);
         while (qs >= kBatch) {
@@ -745,7 +914,6 @@ void search_kernel(SearchArgs a) {
         if (has) {
             const int slot = (ring_head + k) & (kRing - 1);
             r_start[slot] = start;
-            r_vbeg[slot] = v_total + incl - len;
             r_vend[slot] = v_total + incl;
         }
         ring_head += __popcll(mask);
@@ -978,6 +1146,12 @@ void search_kernel(SearchArgs a) {
     }
 }
 
+static unsigned f32_bits(float f) {
+    unsigned u;
+    std::memcpy(&u, &f, sizeof(u));
+    return u;
+}
+
 template <int DS, bool REV, bool BF>
 static void launch_one(const SearchArgs& a, hipStream_t s) {
     if (a.counters)
@@ -995,7 +1169,7 @@ static void launch_ds(const SearchArgs& a, bool bf, hipStream_t s) {
 int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
                   const int* cell_of, const int* start, const void* frame_ws, int N, int D, int K,
                   const frnn_plan_t& plan, unsigned long long* lists, int cap, unsigned long long* counters,
-                  hipStream_t s, const QuerySet* queries) {
+                  unsigned* status, hipStream_t s, const QuerySet* queries) {
     if (N <= 0) return 0;
     const bool bf = plan.path == FRNN_PATH_BRUTEFORCE;
     const QuerySet self{aos, frows, sorted_idx, cell_of, N};
@@ -1005,7 +1179,9 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     if (!bf && (plan.grid_dim < 1 || plan.grid_dim > kMaxG || !sorted_idx || !cell_of || !start)) return 1;
     if (!bf && frame_ws && plan.grid_dim > kFrameGrid) return 1;
     if (!bf && aos_stride(D) >= 16 && plan.grid_dim > kFrameGrid) return 1;   // kernels size s_qg for g <= 4
-    if (cap < list_capacity(K) || K > FRNN_MAX_K || !stats_ws || D < 1 || D > FRNN_MAX_DIM) return 1;
+    // a list must hold the K results; below list_capacity(K) a round can
+    // overflow it, which the capacity guard reports through `status`
+    if (K < 1 || cap < K || K > FRNN_MAX_K || !stats_ws || D < 1 || D > FRNN_MAX_DIM) return 1;
     if (uses_filter_rows(D) && !frows) return 1;
     SearchArgs a{};
     a.pts = aos;
@@ -1021,11 +1197,16 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     a.qcell_of = Q.cell_of;
     a.lists = lists;
     a.counters = counters;
+    a.status = status;
     a.N = N;
     a.M = Q.M;
     a.K = K;
     a.cap = cap;
-    a.room = min(cap, 4 * kWave);
+    a.room = min(cap, kMaxRoom);
+    // the histogram's lowest bucket edge stays positive unless r2 < 2^-123
+    a.r2bits = f32_bits(plan.r2);
+    a.hist_on = a.r2bits >= ((unsigned)kHB << kHS) ? 1 : 0;
+    a.exact_limit = (K + a.room - kBatch) / 2;
     a.G = bf ? 0 : plan.grid_dim;
     a.res = bf ? 1 : plan.res;
     {

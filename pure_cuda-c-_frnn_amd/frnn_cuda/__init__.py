@@ -13,9 +13,16 @@ reference's nanobind binding (python_interface/nanobind_module.cu:8-21):
 Errors the reference never reported (its launch wrappers return void) raise
 ValueError for bad arguments and RuntimeError for device failures.  There is
 no CPU fallback: without the built library or a visible GPU the calls raise.
+
+Threading: ctypes releases the GIL around every library call, so each engine
+serialises its own calls with a lock; calls on one engine from several Python
+threads run one at a time, as they did under the reference's binding, which
+holds the GIL (nanobind_module.cu:11-19).  Separate engines run concurrently.
 """
 import ctypes
+import functools
 import os
+import threading
 
 import numpy as np
 
@@ -49,6 +56,12 @@ class _Plan(ctypes.Structure):
         return {"path": PATH_NAMES.get(self.path, str(self.path)), "grid_dim": self.grid_dim,
                 "res": self.res, "rev_order": self.rev_order, "cells": self.cells,
                 "r2": self.r2, "cell_size": self.cell_size, "inv_cell": self.inv_cell}
+
+
+class Queries(ctypes.Structure):
+    """frnn_queries_t: M separate queries for frnn_launch_find_nbrs (device pointers)."""
+    _fields_ = [("M", ctypes.c_int), ("d_aos", ctypes.c_void_p), ("d_frows", ctypes.c_void_p),
+                ("d_sorted_idx", ctypes.c_void_p), ("d_cell_of", ctypes.c_void_p)]
 
 
 FRAME_TERMS = 32
@@ -126,7 +139,7 @@ def _load():
         "frnn_launch_transpose": ([vp, i32, i32, vp, vp, vp, vp], i32),
         "frnn_uses_filter_rows": ([i32], i32),
         "frnn_launch_find_nbrs": ([vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, ctypes.POINTER(_Plan),
-                                   vp, i32, vp, vp], i32),
+                                   ctypes.POINTER(Queries), vp, i32, vp, vp, vp], i32),
         "frnn_launch_unpermute": ([vp, i32, vp, i32, i32, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
@@ -182,10 +195,21 @@ def scan_partials_count(n):
     return _load().frnn_scan_partials_count(int(n))
 
 
+def _serialised(method):
+    """Run an engine method under the engine's lock (the engine's device
+    buffers, built grid and results are shared state)."""
+    @functools.wraps(method)
+    def call(self, *args, **kwargs):
+        with self._lock:
+            return method(self, *args, **kwargs)
+    return call
+
+
 class FRNNEngine:
     """N-dimensional fixed-radius K-nearest search engine (reference: frnn_engine.h:9-55)."""
 
     def __init__(self, max_points):
+        self._lock = threading.RLock()
         L = _load()
         h = ctypes.c_void_p()
         _check(L.frnn_engine_create(int(max_points), ctypes.byref(h)), "FRNNEngine")
@@ -199,6 +223,7 @@ class FRNNEngine:
         idx, dist = self.search_numpy(points, K, radius)
         return idx.reshape(-1).tolist(), dist.reshape(-1).tolist()
 
+    @_serialised
     def search_gpu(self, dev_ptr, N, dim, K, radius):
         """Device path: SoA fp32 device pointer p[d*N + i] -> (d_idxs_ptr, d_dists_ptr),
         engine-owned SoA [k*N + i] buffers valid until the next call (frnn_engine.cu:195-250)."""
@@ -208,6 +233,7 @@ class FRNNEngine:
                                               ctypes.byref(di), ctypes.byref(dd)), "search_gpu")
         return int(di.value or 0), int(dd.value or 0)
 
+    @_serialised
     def search_gpu_queries(self, points_ptr, N, queries_ptr, M, dim, K, radius):
         """Separate queries: SoA fp32 device pointers to N points p[d*N + i] and M
         queries q[d*M + j] -> (d_idxs_ptr, d_dists_ptr), engine-owned SoA
@@ -220,12 +246,14 @@ class FRNNEngine:
                "search_gpu_queries")
         return int(di.value or 0), int(dd.value or 0)
 
+    @_serialised
     def build(self, points_ptr, N, dim, K, radius):
         """Build the grid of N points (SoA fp32 device pointer p[d*N + i]) once,
         for any number of query() calls with this K and radius."""
         _check(_load().frnn_engine_build(self._handle(), ctypes.c_void_p(int(points_ptr)), int(N), int(dim),
                                          int(K), float(radius)), "build")
 
+    @_serialised
     def query(self, queries_ptr, M):
         """Search M queries (SoA fp32 device pointer q[d*M + j]) against the last
         built grid -> (d_idxs_ptr, d_dists_ptr), SoA [k*M + j]."""
@@ -241,6 +269,7 @@ class FRNNEngine:
         return idx.tolist(), dist.tolist()
 
     # -- numpy conveniences (same semantics, no list conversion) -----------------
+    @_serialised
     def search_numpy(self, points, K, radius):
         """Host path returning ([max_points, K] int32, [max_points, K] float32)."""
         pts = np.ascontiguousarray(np.asarray(points, dtype=np.float32).reshape(-1))
@@ -258,6 +287,7 @@ class FRNNEngine:
                                           dist.ctypes.data_as(ctypes.c_void_p)), "search")
         return idx, dist
 
+    @_serialised
     def get_results_numpy(self, N, K):
         n = int(N) * int(K)
         idx = np.empty(max(n, 0), dtype=np.int32)
@@ -268,22 +298,26 @@ class FRNNEngine:
         return idx, dist
 
     # -- engine controls ----------------------------------------------------------
+    @_serialised
     def set_stream(self, stream):
         """Launch on a HIP stream (int handle, e.g. torch.cuda.current_stream().cuda_stream)."""
         _check(_load().frnn_engine_set_stream(self._handle(), ctypes.c_void_p(int(stream or 0))),
                "set_stream")
 
+    @_serialised
     def last_plan(self):
         p = _Plan()
         _check(_load().frnn_engine_last_plan(self._handle(), ctypes.byref(p)), "last_plan")
         return p.as_dict()
 
+    @_serialised
     def set_profiling(self, enable=True, counters=True):
         """enable: per-stage HIP event times (stage_times()); counters: also run
         the counting build of the search kernel (counters())."""
         flags = (PROFILE_EVENTS | (PROFILE_COUNTERS if counters else 0)) if enable else 0
         _check(_load().frnn_engine_set_profiling(self._handle(), flags), "set_profiling")
 
+    @_serialised
     def stage_times(self):
         """Per-stage milliseconds of the last profiled search (HIP events)."""
         ms = np.zeros(NUM_STAGES, dtype=np.float32)
@@ -291,6 +325,7 @@ class FRNNEngine:
                                                NUM_STAGES), "stage_times")
         return dict(zip(STAGE_NAMES, (float(x) for x in ms)))
 
+    @_serialised
     def counters(self):
         c = np.zeros(NUM_COUNTERS, dtype=np.int64)
         _check(_load().frnn_engine_counters(self._handle(), c.ctypes.data_as(ctypes.c_void_p),
@@ -298,6 +333,7 @@ class FRNNEngine:
         return {"shell_candidates": int(c[0]), "filter_hits": int(c[1]), "accepted": int(c[2]),
                 "streamed_pairs": int(c[3])}
 
+    @_serialised
     def close(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:

@@ -82,7 +82,7 @@ def test_geometry_helpers():
     assert [frnn_cuda.aos_stride(d) for d in (1, 3, 4, 5, 12, 16, 17, 33, 128)] == \
         [4, 4, 4, 8, 12, 16, 32, 64, 128]
     assert frnn_cuda.aos_stride(0) == -1 and frnn_cuda.aos_stride(129) == -1
-    assert [frnn_cuda.list_capacity(k) for k in (1, 32, 64, 65, 128)] == [160, 160, 160, 161, 224]
+    assert [frnn_cuda.list_capacity(k) for k in (1, 32, 64, 65, 128)] == [256] * 5
     assert frnn_cuda.list_capacity(0) == -1
     assert frnn_cuda.scan_partials_count(1_000_001) == 246
 
@@ -111,7 +111,7 @@ def test_launch_seam_rejects_bad_geometry_without_touching_the_device():
     assert L.frnn_launch_frame(None, 10, 12, ctypes.byref(p), None, None, None) == 1   # null pointers
     p.cells = 5
     assert L.frnn_launch_find_nbrs(None, None, None, None, None, None, None, 100000, 12, 32, ctypes.byref(p),
-                                   None, 128, None, None) == 1
+                                   None, None, 128, None, None, None) == 1
     assert L.frnn_launch_frame(None, 10, 12, ctypes.byref(p), None, None, None) == 1   # inconsistent plan
     q = frnn_cuda._Plan()
     assert L.frnn_make_plan(100000, 3, 16, ctypes.c_float(0.1), ctypes.byref(q)) == 0

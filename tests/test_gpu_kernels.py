@@ -426,7 +426,7 @@ def test_seam_search_first_coordinate_plan(framed):
     cap = frnn_cuda.list_capacity(K)
     lists = t.empty(N * cap, dtype=t.int64, device="cuda:0")
     assert L.frnn_launch_find_nbrs(vp(aos), None, vp(sws), vp(sidx), vp(cell_of), vp(start), vp(ws),
-                                   N, D, K, ctypes.byref(plan), vp(lists), cap, None, None) == 0
+                                   N, D, K, ctypes.byref(plan), None, vp(lists), cap, None, None, None) == 0
     idx = t.empty(K * N, dtype=t.int32, device="cuda:0")
     dist = t.empty(K * N, dtype=t.float32, device="cuda:0")
     assert L.frnn_launch_unpermute(vp(lists), cap, vp(inv_p), N, K, vp(idx), vp(dist), None) == 0
