@@ -182,3 +182,38 @@ def test_profiling_enabled_between_build_and_query():
     ri, rd = O.search_queries(X, Q, 32, 0.2)
     assert_rows_equal(gi.reshape(32, 1000).T, gd.reshape(32, 1000).T, ri, rd, "profiled query")
     eng.close()
+
+
+@pytest.mark.parametrize("D,k,N,r", [(12, 3, 20000, 0.1), (16, 4, 30000, 0.12)])
+def test_queries_outside_the_points_range_on_a_projected_frame(D, k, N, r):
+    """Queries beyond the points' bounding box, each at fp32 d2 = r2 - 2 .. r2 + 1
+    ulps (reference order) from a boundary point.  The frame's projection
+    margin is bounded on the points (R = the points' spread); such a query's
+    projection error exceeds it by at most (T+2) u |q - p| for a neighbour p,
+    which the cell edge's r 2^-12 and the window's relative slack absorb."""
+    from test_gpu_margins import _partner_at, _ulps
+    rs = np.random.RandomState(D)
+    X = unit_cloud(N, D, k, 31)
+    r2 = np.float32(np.float32(r) * np.float32(r))
+    # boundary points: the extremes of each coordinate; each query steps out
+    # of the points' box past its point's extreme coordinate
+    far, Q = [], []
+    for j in range(24):
+        d = j % D
+        sign = 1.0 if (j // D) % 2 == 0 else -1.0
+        p = int(np.argmax(sign * X[:, d]))
+        e = np.zeros(D)
+        e[d] = sign
+        t = _ulps(r2, (-2, -1, 0, 1)[j % 4])
+        far.append(p)
+        Q.append(_partner_at(X[p], t, 2e-6, rs, direction=e))
+    Q = np.array(Q, np.float32)
+    lo, hi = X.min(0), X.max(0)
+    assert np.all(np.any((Q < lo) | (Q > hi), axis=1)), "every query lies outside the points' box"
+    log(f"outside queries D={D} N={N} M={len(Q)} r={r}")
+    gi, gd, plan = engine_search_queries(X, Q, 16, r)
+    assert plan["path"] == "grid_first"
+    ri, rd = O.search_queries(X, Q, 16, r)
+    assert_rows_equal(gi, gd, ri, rd, f"outside D={D}")
+    for j, p in enumerate(far):
+        assert (p in gi[j]) == (j % 4 < 2)

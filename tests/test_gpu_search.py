@@ -300,3 +300,57 @@ def test_baseline_configs_full_size(name, nq):
     ri, rd = O.search(w.X, w.K, w.radius, query_ids=q)
     assert_rows_equal(gi[q], gd[q], ri, rd, f"{name} sampled")
     log(f"  path={plan['path']} mean neighbours={(gi >= 0).sum(1).mean():.1f}")
+
+
+@pytest.mark.parametrize("name", ["C1", "C2"])
+def test_baseline_configs_all_rows(name):
+    """Every row of the full-size C1 and C2 searches against the oracle run
+    over the full database (all 200 000 / 1 000 000 queries)."""
+    w = W.config(name)
+    log(f"all rows {name}: N={w.N} D={w.D} K={w.K} r={w.radius:.6f}")
+    gi, gd, plan = engine_search(w.X, w.K, w.radius)
+    assert plan["path"] == "grid_full"
+    ri, rd = O.search(w.X, w.K, w.radius)
+    assert_rows_equal(gi, gd, ri, rd, f"{name} all rows")
+
+
+@pytest.mark.parametrize("D,k,N,r,K", [(64, 4, 1500, 0.6, 32), (128, 4, 1200, 0.8, 128), (40, 4, 1000, 0.5, 16)])
+def test_host_search_wide_rows(D, k, N, r, K):
+    """The host path search() at D > 32, where the reference's staging buffer
+    (d_points, sized for 32 coordinates: frnn_engine.cu:26-28, written at
+    :113-117) overflows; here the staging grows with D."""
+    X = unit_cloud(N, D, k, 61)
+    eng = frnn_cuda.FRNNEngine(max_points=N)
+    log(f"host search D={D} N={N} K={K} r={r}")
+    idx, dist = eng.search_numpy(X.reshape(-1), K, r)
+    eng.close()
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(idx, dist, ri, rd, f"host search D={D}")
+
+
+def test_concurrent_calls_on_one_engine_are_serialised():
+    """Python threads sharing one engine: every call runs whole (the binding
+    serialises them; the reference's binding held the GIL), so each thread's
+    host-path results match the oracle for its own input."""
+    import threading
+    eng = frnn_cuda.FRNNEngine(max_points=8000)
+    inputs = [(unit_cloud(8000, 3, 3, 70 + i), 16, 0.05 + 0.01 * i) for i in range(4)]
+    refs = [O.search(X, K, r) for X, K, r in inputs]
+    errors = []
+
+    def worker(i):
+        X, K, r = inputs[i]
+        try:
+            for _ in range(3):
+                idx, dist = eng.search_numpy(X.reshape(-1), K, r)
+                assert_rows_equal(idx, dist, refs[i][0], refs[i][1], f"thread {i}")
+        except Exception as e:          # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    eng.close()
+    assert not errors, errors[0]

@@ -264,3 +264,35 @@ def test_oracle_padding_and_self():
     r2 = np.float32(np.float32(0.05) * np.float32(0.05))
     assert list(idx[0]) == [0, 2, -1, -1] and list(idx[1]) == [1, -1, -1, -1]
     assert dist[0][0] == 0 and np.all(dist[1][1:] == r2)
+
+
+@pytest.mark.parametrize("D,k,N,r,K", [(3, 3, 3000, 0.08, 16), (2, 2, 2500, 0.05, 8), (12, 3, 4000, 0.2, 32),
+                                       (5, 5, 2000, 0.3, 16)])
+def test_oracle_shell_candidates_closed_form(D, k, N, r, K):
+    """oracle_shell_candidates (the reference's unpruned 3^g shell size per
+    query, find_nbrs.cu:167-187 / :288-304) against a numpy count: clamped
+    cells of every point on the plan's grid, a bincount, and for every query
+    the sum of the counts of its in-range neighbouring cells."""
+    X = unit_cloud(N, D, k, 5)
+    X[:40, 0] = 1.0                                    # closed upper cell
+    p = O.plan(N, D, K, r)
+    assert p["path"] in ("grid_full", "grid_first")
+    g, res = p["grid_dim"], p["res"]
+    inv = np.float32(1.0) / np.float32(r)
+    coords = np.clip(np.floor(X[:, :g] * inv), 0, res - 1).astype(np.int64)
+    cell = (coords * (res ** np.arange(g))[None, :]).sum(1)
+    cnt = np.bincount(cell, minlength=res ** g)
+    total = 0
+    offsets = np.array(np.meshgrid(*[[-1, 0, 1]] * g, indexing="ij")).reshape(g, -1).T
+    for o in offsets:
+        nb = coords + o[None, :]
+        ok = np.all((nb >= 0) & (nb < res), axis=1)
+        total += int(cnt[(nb[ok] * (res ** np.arange(g))[None, :]).sum(1)].sum())
+    assert O.shell_candidates(X, K, r) == total
+    q = np.array([0, 5, 17, N - 1], dtype=np.int32)
+    sub = 0
+    for o in offsets:
+        nb = coords[q] + o[None, :]
+        ok = np.all((nb >= 0) & (nb < res), axis=1)
+        sub += int(cnt[(nb[ok] * (res ** np.arange(g))[None, :]).sum(1)].sum())
+    assert O.shell_candidates(X, K, r, query_ids=q) == sub
