@@ -234,6 +234,18 @@ int frnn_launch_bin_count(const float* d_points_soa, int N, int grid_dim, int re
 int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partials,
                                void* stream);
 
+/* No counterpart in the reference: frnn_launch_exclusive_scan without the
+ * d_partials workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It calls no allocating routine: the per-tile partial sums live
+ * in a fixed 16 KB device array inside the library (one per device, kept
+ * until the process ends).  n <= FRNN_SCAN_NOALLOC_MAX_N, else
+ * FRNN_ERR_CAPACITY.  All calls on one device share that array, so calls that
+ * overlap on a device (concurrent streams or threads) race; calls in sequence
+ * on one stream are safe.  Results equal frnn_launch_exclusive_scan's. */
+#define FRNN_SCAN_NOALLOC_MAX_N 16777216
+int frnn_launch_exclusive_scan_noalloc(const int* d_in, int n, int* d_out, void* stream);
+
 /* Per-coordinate statistics of the input (no reference counterpart): mean,
  * variance, minimum and maximum of every coordinate, accumulated in fp64 in a
  * fixed order.  Needs frnn_stats_workspace_bytes(dim) bytes at d_stats_ws. */

@@ -13,6 +13,8 @@
 //     4-byte stores into SoA planes, and also records the inverse permutation;
 //   * the scan is a three-phase reduce/scan/propagate over 4096-element tiles
 //     (16-byte coalesced accesses) with no inter-block spin waits.
+#include <mutex>
+
 #include "frnn_device.hpp"
 #include "frnn_internal.hpp"
 
@@ -883,6 +885,56 @@ int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, co
 }
 
 int scan_partials_count(int n) { return (n + kScanTile - 1) / kScanTile + 1; }
+
+// ---- allocation-free scan ----------------------------------------------------
+// The scan's only scratch is one partial sum per tile of kScanTile ints, at most
+// kScanTile of them (n <= kScanTile^2).  launch_exclusive_scan_noalloc keeps
+// them in this file-scope device array (16 KB per device, held until the
+// process ends) instead of a caller's workspace.  In host code `scratch` names
+// a host-side stand-in, not a device address: the device address of each
+// device's copy comes from hipGetSymbolAddress, looked up once per device
+// (with that device current, on its first call) and used for every kernel
+// argument.  Every call on one device shares the array: calls that overlap on
+// a device race.  Nothing in it needs clearing: the reduce pass writes every
+// partial the later passes read.
+static __device__ __align__(256) int scratch[kScanTile];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int* g_scratch_dev[kMaxDevices] = {};
+hipError_t g_scratch_err = hipSuccess;
+}  // namespace
+
+int scan_noalloc_max() { return kScanTile * kScanTile; }
+
+int launch_exclusive_scan_noalloc(const int* in, int n, int* out, hipStream_t s) {
+    if (n <= 0) return 0;
+    if (n > scan_noalloc_max()) return 2;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        g_scratch_err = e != hipSuccess ? e : hipErrorInvalidDevice;
+        return 4;
+    }
+    int* p = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_dev[dev]) {
+            void* a = nullptr;
+            e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !a) {
+                g_scratch_err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+                return 4;
+            }
+            g_scratch_dev[dev] = static_cast<int*>(a);
+        }
+        p = g_scratch_dev[dev];
+    }
+    return launch_exclusive_scan(in, n, out, p, s);
+}
+
+hipError_t scan_noalloc_error() { return g_scratch_err; }
 
 int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s) {
     if (n <= 0) return 0;

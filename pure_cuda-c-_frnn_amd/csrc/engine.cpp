@@ -685,6 +685,17 @@ int frnn_launch_exclusive_scan(const int* d_in, int n, int* d_out, int* d_partia
                          "scan launch");
 }
 
+int frnn_launch_exclusive_scan_noalloc(const int* d_in, int n, int* d_out, void* stream) {
+    if (n < 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "n must be >= 0");
+    if (n > frnn::scan_noalloc_max())
+        return fail(FRNN_ERR_CAPACITY, "n exceeds FRNN_SCAN_NOALLOC_MAX_N (16777216 = 4096 tiles of 4096 ints; "
+                                       "the partial sums live in a fixed 16 KB device scratch)");
+    if (n > 0 && (!d_in || !d_out)) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device pointer");
+    const int rc = frnn::launch_exclusive_scan_noalloc(d_in, n, d_out, (hipStream_t)stream);
+    if (rc == 4) return hip_fail(frnn::scan_noalloc_error(), "looking up the scan scratch's device address");
+    return launch_status(rc, "allocation-free scan launch");
+}
+
 long long frnn_stats_workspace_bytes(int dim) {
     if (dim < 1 || dim > FRNN_MAX_DIM) return -1;
     return (long long)frnn::stats_layout(dim).total;

@@ -133,6 +133,13 @@ int launch_fill_i32(int* p, long long n, int v, hipStream_t s);
 int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, const void* frame_ws,
                      int cells, int* cell_of, int* rank, int* cnt, hipStream_t s);
 int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s);
+// The same scan with its partial sums in a file-scope device scratch array
+// (no workspace argument, no allocation); n <= scan_noalloc_max().  Returns
+// 0, 2 (n too large), 3 (launch error) or 4 (the scratch's device address
+// could not be looked up: scan_noalloc_error()).
+int launch_exclusive_scan_noalloc(const int* in, int n, int* out, hipStream_t s);
+int scan_noalloc_max();
+hipError_t scan_noalloc_error();
 // With frows (which needs stats_ws) the centred filter rows fl(x - mean) are
 // written too.
 int launch_reorder(const float* pts, int N, int D, const int* cell_of, const int* rank, const int* start,

@@ -131,6 +131,7 @@ def _load():
         "frnn_grid_cells": ([i32, i32, ctypes.POINTER(_Plan)], i64),
         "frnn_launch_bin_count": ([vp, i32, i32, i32, f32, i64, vp, vp, vp, vp, vp], i32),
         "frnn_launch_exclusive_scan": ([vp, i32, vp, vp, vp], i32),
+        "frnn_launch_exclusive_scan_noalloc": ([vp, i32, vp, vp], i32),
         "frnn_stats_workspace_bytes": ([i32], i64),
         "frnn_launch_point_stats": ([vp, i32, i32, vp, vp], i32),
         "frnn_frame_workspace_bytes": ([i32, i32, ctypes.POINTER(_Plan)], i64),
