@@ -9,20 +9,27 @@ in HBM and the outputs left in HBM -- the timing the reference's harness uses
 (Tests/scripts/benchmark_vs_libfrnn.py:146-169).  Prints ONE JSON line on stdout:
 
   value            mean ms per step over exactly K steps (sync before and after)
-  roofline         dominant kernel (the neighbour search): fp32 flops of its
-                   distance filter -- 2*D per (query, candidate) pair streamed
-                   through the filter, counted live by the kernel -- / its mean
-                   HIP-event duration, against the fp32 MFMA peak; traffic (HBM
-                   bytes per launch) from the committed rocprofv3 PMC summary when
-                   present.  hbm_view: the search's algorithmic bytes
-                   8DN + 4(C+1) + 4N + 8KN (read rows, cell offsets, index map;
-                   write K keys per query) over the same duration vs 8 TB/s.
+  roofline         dominant kernel (the neighbour search), its mean HIP-event
+                   duration on the engine's stream over the timed steps:
+                   grid paths: bound "hbm", the search's algorithmic bytes
+                   8DN + 4(C+1) + 4N + 8KN (read the rows, the cell offsets and
+                   the index map; write K keys per query; C = the plan's cells)
+                   per launch / duration vs 8 TB/s;
+                   brute force: bound "mfma", 2 * N * N * D flops / duration vs
+                   the fp32 MFMA peak.  The other view is reported beside it
+                   (mfma_view: 2*D flops per (query, candidate) pair streamed
+                   through the MFMA filter, counted by the kernel; hbm_view).
+                   traffic: HBM bytes per launch from the committed rocprofv3
+                   PMC summary for this config, when present.
   build_hbm        grid-build kernels: algorithmic bytes / event time vs 8 TB/s
   refD<D>N<N>      a cell of the reference's own published K=16 sweep (A100
                    latency reported beside ours; frnn_workloads.REF_SWEEP)
-  cpu_baseline     the C++/OpenMP restatement (oracle/) on a bounded query sample,
-                   timed on this host, extrapolated to all N queries; the same
-                   sample is also compared bit-exactly with the GPU rows
+  cpu_baseline     the C++/OpenMP restatement of the reference (oracle/: the
+                   reference's own grid, i.e. its first-coordinate grid on the
+                   raw coordinates for D > 4) on every host core this job may
+                   use, on a bounded query sample timed on this host and scaled
+                   to all N queries; the same sample is compared bit-exactly with
+                   the GPU rows
 """
 import argparse
 import json
@@ -90,12 +97,22 @@ def cpu_baseline(w, gi, gd, target_s, threads):
     same = np.all(gi[q] == ri, 1) & np.all(gd[q].view(np.uint32) == rd.view(np.uint32), 1)
     return {
         "value": round(full_ms, 3), "unit": "ms", "cores": threads, "kind": "port",
+        "algorithm": "the reference's (oracle/frnn_oracle.cpp): its grid on the raw coordinates (for D > 4 the "
+                     "first-coordinate grid, g = 4), the full 3^g cell shell per query, sequential-fma distances",
         "sample": f"{nq} of {w.N} queries (random, seed 99) against the full database, with the "
                   f"full grid build; search time scaled by N/{nq}: build {build_s * 1e3:.1f} ms + "
                   f"search {search_s:.2f} s",
         "speedup_vs_gpu": None, "parity_sample_rows": nq,
         "parity_mismatched_rows": int(np.sum(~same)),
     }
+
+
+def host_cores():
+    """CPUs this process may run on (the job's share of the host)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
 
 
 def bench_queries(args, w):
@@ -128,9 +145,13 @@ def bench_queries(args, w):
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
     ms = 1e3 * float(np.mean(times))
-    eng.set_profiling(True, counters=True)
+    # one profiled query() with the plain kernel for the stage times, then one
+    # with the counting build for the work counters
+    eng.set_profiling(True, counters=False)
     eng.query(dq.data_ptr(), M)
     st = eng.stage_times()
+    eng.set_profiling(True, counters=True)
+    eng.query(dq.data_ptr(), M)
     ct = eng.counters()
     plan = eng.last_plan()
     eng.close()
@@ -143,6 +164,7 @@ def bench_queries(args, w):
         "config": {"workload": w.name, "N": w.N, "M": M, "D": w.D, "K": w.K, "radius": w.radius,
                    "path": plan["path"]},
         "search_kernel_ms": round(st["search"], 4),
+        "query_build_ms": round(st["reorder"], 4),
         "counters": {k: int(v) for k, v in ct.items()},
     }))
 
@@ -227,24 +249,38 @@ def main():
     gi = idx.reshape(w.K, w.N).T
     gd = dist.reshape(w.K, w.N).T
 
-    # dominant kernel roofline: fp32 MFMA over the pairs the distance filter evaluates
-    pairs = ctr["streamed_pairs"]
-    flops = 2.0 * w.D * pairs
+    # dominant kernel (the search): algorithmic work per launch / its mean
+    # HIP-event duration.  Grid paths are priced on HBM bytes, brute force on
+    # fp32 MFMA flops; the other view is reported beside it.
     search_s = stages["search"] / 1e3
-    achieved = flops / search_s / 1e12
+    pairs = ctr["streamed_pairs"]
+    filt_flops = 2.0 * w.D * pairs
+    filt_tf = filt_flops / search_s / 1e12
+    mfma_view = {"flops_per_launch": filt_flops, "filtered_pairs": pairs,
+                 "TFLOPs": round(filt_tf, 3), "frac": round(filt_tf / MFMA_F32_PEAK_TFLOPS, 4),
+                 "unit_of_work": "2*D flops per (query, candidate) pair streamed through the MFMA filter"}
     traffic, traffic_src = traffic_from_profiles(args.config)
-    C = frnn_cuda.grid_cells(w.N, w.D, w.K, w.radius)
+    C = plan["cells"] if plan["path"] != "bruteforce" else 0
     alg_bytes = 8 * w.D * w.N + 4 * (C + 1) + 4 * w.N + 8 * w.K * w.N
     alg_gbs = alg_bytes / search_s / 1e9
-    roofline = {"kernel": "search_kernel (neighbour search)", "bound": "mfma",
-                "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 4), "traffic": traffic,
-                "flops_per_launch": flops, "filtered_pairs": pairs,
-                "shell_candidate_pairs": ctr["shell_candidates"],
-                "mean_kernel_ms": round(stages["search"], 4),
-                "traffic_source": traffic_src,
-                "hbm_view": {"algorithmic_bytes": alg_bytes, "GBps": round(alg_gbs, 1),
-                             "frac": round(alg_gbs / HBM_PEAK_GBS, 5)}}
+    hbm_view = {"algorithmic_bytes": alg_bytes, "GBps": round(alg_gbs, 1),
+                "frac": round(alg_gbs / HBM_PEAK_GBS, 5),
+                "bytes_formula": "8DN + 4(C+1) + 4N + 8KN, C = the plan's cells"}
+    if plan["path"] == "bruteforce":
+        bf_flops = 2.0 * w.N * w.N * w.D
+        tf = bf_flops / search_s / 1e12
+        roofline = {"kernel": "search_kernel (tiled brute force, fp32 MFMA distance filter)", "bound": "mfma",
+                    "achieved": round(tf, 3), "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4), "traffic": traffic,
+                    "flops_per_launch": bf_flops, "mean_kernel_ms": round(stages["search"], 4),
+                    "traffic_source": traffic_src, "hbm_view": hbm_view}
+    else:
+        roofline = {"kernel": "search_kernel (neighbour search)", "bound": "hbm",
+                    "achieved": round(alg_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(alg_gbs / HBM_PEAK_GBS, 5), "traffic": traffic,
+                    "algorithmic_bytes": alg_bytes, "mean_kernel_ms": round(stages["search"], 4),
+                    "traffic_source": traffic_src, "mfma_view": mfma_view,
+                    "shell_candidate_pairs": ctr["shell_candidates"]}
 
     if plan["path"] != "bruteforce":
         bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"],
@@ -270,7 +306,7 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
+        threads = host_cores()
         eprint(f"[bench] cpu baseline with {threads} threads (~{args.cpu_seconds:.0f}s sample)")
         cpu = cpu_baseline(w, gi, gd, args.cpu_seconds, threads)
         cpu["speedup_vs_gpu"] = round(cpu["value"] / ms_per_step, 1)

@@ -193,8 +193,8 @@ int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
  * 0 zero-fill, 1 point statistics, 2 grid frame, 3 bin+count, 4 scan,
  * 5 reorder/transpose (and, for separate queries, their binning, scan and
  * reorder), 6 neighbour search, 7 unpermute.  After frnn_engine_query, stages
- * 0-4 are those of the build call and stage 5 runs from the build's reorder
- * to this call's search. */
+ * 0-4 read 0 (they belong to the build) and stage 5 is the queries' own
+ * binning, scan and reorder. */
 #define FRNN_NUM_STAGES 8
 #define FRNN_PROFILE_EVENTS 1
 #define FRNN_PROFILE_COUNTERS 2

@@ -25,7 +25,7 @@
 //   * brute force uses the sequential-fma order (the reference's float4 grouping
 //     at no_grid_frnn.cu:84-106 leaves contraction to the compiler).
 //
-// Build: see oracle/Makefile (g++ -O2 -fopenmp -ffp-contract=off).
+// Build: see oracle/Makefile (g++ -O3 -mfma -fopenmp -ffp-contract=off).
 
 #include <algorithm>
 #include <chrono>

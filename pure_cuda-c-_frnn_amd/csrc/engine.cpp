@@ -265,7 +265,10 @@ int build_points(frnn_engine* e, BuiltGrid& b, const float* d_pts, int N, int di
 // Stages 6-7 against a built grid: every point as a query (sep false), or
 // the M queries d_q (SoA [d*M + j]), first binned on the points' grid and
 // reordered into their own search order (part of stage 5).
-int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, int M) {
+// own_prep: a call that only queries a grid built earlier (frnn_engine_query):
+// its stage 5 is the queries' own binning, scan and reorder, and stages 0-4
+// (the build's) read 0.
+int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, int M, bool own_prep = false) {
     const int Mq = sep ? M : b.N;   // queries = result rows
     const int K = b.K;
     e->has_result = false;
@@ -303,6 +306,10 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
     // search order, or transposed for brute force; their filter rows are
     // centred on the points' mean, as the points' are
     frnn::QuerySet qs{};
+    if (own_prep) {
+        for (int i = 0; i <= 5; ++i) e->ev_recorded[i] = false;
+        ST_TRY(mark_stage(e, 5));
+    }
     if (sep) {
         ST_TRY(grow(&e->q_aos, &e->q_aos_bytes, (size_t)M * ds, "allocating query rows"));
         float* q_frows = nullptr;
@@ -571,7 +578,7 @@ int frnn_engine_query(frnn_engine_t* e, const float* d_queries, int M, int** d_i
     if (M > e->max_p) return fail(FRNN_ERR_CAPACITY, "M exceeds max_points");
     if (!d_queries && M > 0) return fail(FRNN_ERR_INVALID_ARGUMENT, "null device queries");
     e->last_plan = e->built.ref_plan;
-    ST_TRY(run_queries(e, e->built, true, d_queries, M));
+    ST_TRY(run_queries(e, e->built, true, d_queries, M, true));
     if (d_idxs) *d_idxs = e->out_idx;
     if (d_dists) *d_dists = e->out_dist;
     return FRNN_OK;

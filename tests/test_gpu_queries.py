@@ -177,7 +177,16 @@ def test_profiling_enabled_between_build_and_query():
     eng.query(dq.data_ptr(), 1000)
     st = eng.stage_times()
     assert st["bin_count"] == 0 and st["search"] > 0 and st["unpermute"] > 0
+    # stage 5 of a query() call is the queries' own binning, scan and reorder
+    assert st["reorder"] > 0
     assert eng.counters()["accepted"] > 0
+    # a profiled build, then a query: the query's stage times cover only its
+    # own work (the build's stages read 0 after it)
+    eng.build(d.data_ptr(), 3000, 16, 32, 0.2)
+    eng.query(dq.data_ptr(), 1000)
+    st = eng.stage_times()
+    assert st["zero_fill"] == 0 and st["stats"] == 0 and st["scan"] == 0
+    assert st["reorder"] > 0 and st["search"] > 0
     gi, gd = eng.get_results_numpy(1000, 32)
     ri, rd = O.search_queries(X, Q, 32, 0.2)
     assert_rows_equal(gi.reshape(32, 1000).T, gd.reshape(32, 1000).T, ri, rd, "profiled query")
