@@ -213,10 +213,14 @@ struct WavesPerEU { static constexpr int value = DS <= 4 ? 5 : DS <= 16 ? 4 : 2;
 
 // CNT: the profiling build of the kernel, which also keeps the work counters
 // (a separate instantiation, so the counting code costs the plain kernel no
-// registers).
-template <int DS, bool REV, bool BF, bool CNT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DS>::value)))
+// registers).  NW: waves per workgroup.  One wave for every grid path (each
+// wave streams its own candidates); brute force on wide rows runs NW waves
+// that share each candidate tile through LDS (below).
+template <int DS, bool REV, bool BF, bool CNT, int NW = 1>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WavesPerEU<DS>::value)))
 void search_kernel(SearchArgs a) {
+    constexpr bool MW = NW > 1;
+    static_assert(!MW || (BF && DS >= 64), "shared candidate tiles: brute force on wide rows");
     constexpr int HD = DS / 2;
     constexpr bool PREFETCH = DS <= 32;
     // The chunk's query rows: staged in LDS for DS <= 32; wider rows are read
@@ -227,24 +231,26 @@ void search_kernel(SearchArgs a) {
     constexpr bool kQueryLds = DS <= 32;
     constexpr int RS = (DS % 8 == 0) ? DS + 4 : DS;
     __shared__ __align__(16) float s_q[kQueryLds ? kQB * RS : 4];
-    __shared__ int s_cnt[kQB];
-    __shared__ int s_srt[kQB];       // sorted prefix length of each list
-    __shared__ unsigned long long s_thr[kQB];
+    // Per-wave state (one slice per wave of the workgroup): list lengths,
+    // sorted prefix lengths, thresholds, histograms, counters and the queue.
+    __shared__ int s_cnt_w[NW * kQB];
+    __shared__ int s_srt_w[NW * kQB];       // sorted prefix length of each list
+    __shared__ unsigned long long s_thr_w[NW * kQB];
     // threshold histograms: byte b of query n's words is its bucket b count;
     // s_hb[n], the lowest bucket whose keys and those below number at least K
     // once that happens (B - 1 before); s_hcle[n], the number of keys in
     // buckets <= s_hb[n].  Every accepted key is below the threshold, which
     // never exceeds bucket s_hb[n]'s upper edge, so it lands in such a bucket.
-    __shared__ unsigned s_hist[kQB * kHW];
-    __shared__ int s_hcle[kQB];
-    __shared__ unsigned char s_hb[kQB];
-    __shared__ unsigned long long s_ctr[5];
+    __shared__ unsigned s_hist_w[NW * kQB * kHW];
+    __shared__ int s_hcle_w[NW * kQB];
+    __shared__ unsigned char s_hb_w[NW * kQB];
+    __shared__ unsigned long long s_ctr_w[NW * 5];
     // Rows of up to 32 floats re-evaluate a tile's hits right after its MFMA
     // chain, from the tile's raw rows staged in LDS; wider rows queue hits as
     // (query, sorted position) and re-evaluate them 64 at a time from memory.
     constexpr bool kTileExact = DS <= 32;
-    __shared__ unsigned char s_qn[kTileExact ? 1 : kQueueCap];
-    __shared__ int s_qpos[kTileExact ? 1 : kQueueCap];
+    __shared__ unsigned char s_qn_w[kTileExact ? 1 : NW * kQueueCap];
+    __shared__ int s_qpos_w[kTileExact ? 1 : NW * kQueueCap];
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points
     // at virtual stream positions [vbeg, vend).  Runs are contiguous in the
     // stream, so a run's vbeg is the vend of the run before it (slot
@@ -257,7 +263,7 @@ void search_kernel(SearchArgs a) {
     // at DS = 16 (four waves per SIMD), where unpadded rows keep the
     // workgroup within a quarter of the LDS per SIMD.
     constexpr int TS = DS == 16 ? DS : RS;
-    __shared__ int t_pos[kTileExact ? 1 : 32];
+    __shared__ int t_pos_w[kTileExact ? 1 : NW * 32];
     __shared__ int t_idx[kTileExact ? 32 : 1];
     __shared__ __align__(16) float t_rows[kTileExact ? 32 * TS : 4];
     // (a tile holds at most 32 x 32 hits; 64 more entries take the writes of
@@ -273,20 +279,48 @@ void search_kernel(SearchArgs a) {
     // a full-D grid needs res^D <= 1M cells with res > 3, so D <= 9)
     constexpr int kGA = DS >= 16 ? kFrameGrid : kMaxG;
     __shared__ float s_qg[BF ? 1 : kQB * kGA];
+    // brute force with shared tiles: two buffers of 32 centred candidate rows,
+    // BRS floats apart (DS + 4: the 16-byte reads of 8 consecutive rows cover
+    // all bank groups)
+    constexpr int BRS = DS + 4;
+    __shared__ __align__(16) float bf_tile[MW ? 2 * 32 * BRS : 4];
 
-    const int lane = threadIdx.x;
+    const int lane = MW ? (int)(threadIdx.x & (kWave - 1)) : (int)threadIdx.x;
+    const int wave = MW ? (int)(threadIdx.x / kWave) : 0;
+    int* const s_cnt = s_cnt_w + wave * kQB;
+    int* const s_srt = s_srt_w + wave * kQB;
+    unsigned long long* const s_thr = s_thr_w + wave * kQB;
+    unsigned* const s_hist = s_hist_w + wave * kQB * kHW;
+    int* const s_hcle = s_hcle_w + wave * kQB;
+    unsigned char* const s_hb = s_hb_w + wave * kQB;
+    unsigned long long* const s_ctr = s_ctr_w + wave * 5;
+    unsigned char* const s_qn = s_qn_w + (kTileExact ? 0 : wave * kQueueCap);
+    int* const s_qpos = s_qpos_w + (kTileExact ? 0 : wave * kQueueCap);
+    int* const t_pos = t_pos_w + (kTileExact ? 0 : wave * 32);
+    // Synchronisation of a wave's own LDS traffic.  A one-wave workgroup uses
+    // the barrier with LDS-only fences; in a multi-wave workgroup the per-wave
+    // code (hits, lists, selection) must not use the workgroup barrier (its
+    // waves reach different numbers of those): one wave's LDS accesses take
+    // effect in program order, so a compiler fence suffices there.
+    auto lsync = [&]() __attribute__((always_inline)) {
+        if constexpr (MW) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local");
+        else lds_sync();
+    };
     const int n = lane & 31;
     const int h = lane >> 5;
     // Workgroup b runs on XCD b % 8, so consecutive chunks of the cell order
     // spread over all XCDs.  Work per chunk follows the point density, and a
     // contiguous range per XCD left the XCDs holding dense regions finishing
-    // up to 2x later than the rest; interleaving keeps them balanced.
-    const int chunk = blockIdx.x;
-    if (chunk >= a.nchunks) return;
+    // up to 2x later than the rest; interleaving keeps them balanced.  A
+    // multi-wave workgroup keeps waves without queries (the last workgroup's)
+    // running: every wave passes the tile barriers.
+    const int chunk = blockIdx.x * NW + wave;
+    if (!MW && chunk >= a.nchunks) return;
     const int q0 = chunk * kQB;
-    const int nq = min(kQB, a.M - q0);
+    // (waves of a multi-wave workgroup past the last chunk have no queries)
+    const int nq = MW ? max(min(kQB, a.M - q0), 0) : min(kQB, a.M - q0);
     const bool qvalid = n < nq;
-    unsigned long long* const lists = a.lists + (size_t)q0 * a.cap;
+    unsigned long long* const lists = a.lists + (size_t)(MW ? min(q0, a.M) : q0) * a.cap;
 
     if constexpr (kQueryLds) {
         const float* src = a.qpts + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
@@ -311,8 +345,8 @@ void search_kernel(SearchArgs a) {
     }
 #pragma unroll
     for (int i = lane; i < kQB * kHW; i += kWave) s_hist[i] = 0u;
-    if (lane == 0) r_vend[kRing - 1] = 0;
-    lds_sync();
+    if (lane == 0 && wave == 0) r_vend[kRing - 1] = 0;
+    lsync();
     // Filter operands are the rows centred on the input mean, fl(x - mean).
     // Rows of up to 32 floats are centred in registers as they are loaded
     // (this lane's half of the means stays in registers); wider rows stream
@@ -338,7 +372,10 @@ void search_kernel(SearchArgs a) {
     float bop[HD + 1];
     float qn2 = 0.0f;
     {
-        const float* qr = (kCentredRows ? a.qfrows : a.qpts) + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
+        // (invalid lanes read a valid row: the chunk's first, or row 0 in a
+        // wave without queries)
+        const int qrow = MW ? (qvalid ? q0 + n : 0) : q0 + (qvalid ? n : 0);
+        const float* qr = (kCentredRows ? a.qfrows : a.qpts) + (size_t)qrow * DS + h * HD;
         float pn = 0.0f;
 #pragma unroll
         for (int j = 0; j < HD; j += 2) {
@@ -403,7 +440,7 @@ void search_kernel(SearchArgs a) {
             atomicAdd(&s_hist[qn * kHW + (b >> 2)], 1u << (8 * (b & 3)));
             atomicAdd(&s_hcle[qn], 1);
         }
-        lds_sync();
+        lsync();
         if (a.hist_on && any && qvalid) {
             int cle = s_hcle[n];
             if (cle >= a.K) {
@@ -512,7 +549,7 @@ void search_kernel(SearchArgs a) {
                 // histogram from them (every kept key is <= the K-th, so in a
                 // bucket <= the K-th key's)
                 if (lane < kHW) s_hist[qn * kHW + lane] = 0u;
-                lds_sync();
+                lsync();
 #pragma unroll
                 for (int e = 0; e < EK; ++e) {
                     const int i = e * kWave + lane;
@@ -527,7 +564,7 @@ void search_kernel(SearchArgs a) {
                 }
             }
         }
-        lds_sync();
+        lsync();
     };
     // Filter compaction of query qn's list: drop the keys above its threshold
     // (they can no longer be among the K results), keeping the order, so the
@@ -557,7 +594,7 @@ void search_kernel(SearchArgs a) {
             s_cnt[qn] = base;
             s_srt[qn] = nm;
         }
-        lds_sync();
+        lsync();
         return base;
     };
     auto select_topk = [&](int qn, bool final_pass) __attribute__((always_inline)) {
@@ -744,7 +781,7 @@ void search_kernel(SearchArgs a) {
     auto hits_tile_exact = [&](const Tile& t, const floatx16& acc, float cand_norm) __attribute__((always_inline)) {
         const bool robust = robust_q || (__ballot(n < t.count && !(cand_norm < 1.0e37f)) != 0);
         if (!any_hit(acc, robust)) return;
-        lds_sync();
+        lsync();
         // both halves store the same values
         t_idx[n] = t.idx;
         {
@@ -785,7 +822,7 @@ void search_kernel(SearchArgs a) {
         }
         bump(1, total);
         if (total == 0) return;
-        lds_sync();
+        lsync();
         for (int base = 0; base < total; base += kWave) {
             make_room();
             bool accepted = false, ovf = false;
@@ -826,9 +863,9 @@ void search_kernel(SearchArgs a) {
             }
         }
         if (__ballot(gh[0] || gh[1] || gh[2] || gh[3]) == 0) return;
-        lds_sync();
+        lsync();
         if (h == 0) t_pos[n] = t.pos;
-        lds_sync();
+        lsync();
         int first, width;
         rows_of(t.v0, t.count, first, width);
 #pragma unroll
@@ -858,7 +895,7 @@ void search_kernel(SearchArgs a) {
             }
         }
         if (q_size > kQueueCap && a.status && lane == 0) a.status[0] = 1u;
-        lds_sync();
+        lsync();
         int qs = min(q_size, kQueueCap);
         while (qs >= kBatch) {
             process_batch(qs - kBatch, kBatch, false);
@@ -918,10 +955,72 @@ void search_kernel(SearchArgs a) {
         }
         ring_head += __popcll(mask);
         v_total += total;
-        lds_sync();
+        lsync();
     };
 
-    if constexpr (BF) {
+    if constexpr (MW) {
+        // Brute force, NW waves per workgroup: every wave streams all N points
+        // in tiles of 32 centred rows, which the workgroup stages once per tile
+        // in LDS (tile t in buffer t & 1).  Each thread loads its share of tile
+        // t + 1 into registers before tile t's MFMA chain and stores it after
+        // the tile's hits; one workgroup barrier per tile separates the two
+        // buffers' uses.  The per-wave hit handling never uses the workgroup
+        // barrier, so every wave passes the same barriers (ntiles of them).
+        bump(0, (unsigned long long)nq * a.N);
+        if (qvalid) q_vend = 0x7fffffff;
+        constexpr int kRowF4 = DS / 4;                    // float4 per row
+        constexpr int kPer = 32 * kRowF4 / (kWave * NW);  // float4 per thread and tile
+        static_assert(32 * kRowF4 % (kWave * NW) == 0, "tile loads split evenly");
+        const int tid = threadIdx.x;
+        const int ntiles = (a.N + 31) / 32;
+        float4 pf[kPer];
+        auto tile_load = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int f = tid + k * kWave * NW;
+                const int p = 32 * t + f / kRowF4;
+                pf[k] = p < a.N ? *reinterpret_cast<const float4*>(a.frows + (size_t)p * DS + 4 * (f % kRowF4))
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        };
+        auto tile_store = [&](int t) __attribute__((always_inline)) {
+            float* buf = bf_tile + (t & 1) * 32 * BRS;
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int f = tid + k * kWave * NW;
+                *reinterpret_cast<float4*>(buf + (f / kRowF4) * BRS + 4 * (f % kRowF4)) = pf[k];
+            }
+        };
+        tile_load(0);
+        tile_store(0);
+        __syncthreads();
+        for (int t = 0; t < ntiles; ++t) {
+            const bool more = t + 1 < ntiles;
+            if (more) tile_load(t + 1);
+            Tile cur;
+            cur.v0 = 32 * t;
+            cur.count = min(32, a.N - 32 * t);
+            cur.pos = cur.v0 + n;
+            cur.idx = -1;
+            {
+                const float* src = bf_tile + (t & 1) * 32 * BRS + n * BRS + h * HD;
+#pragma unroll
+                for (int j = 0; j < HD; j += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(src + j);
+                    cur.op[j] = v.x;
+                    cur.op[j + 1] = v.y;
+                    cur.op[j + 2] = v.z;
+                    cur.op[j + 3] = v.w;
+                }
+            }
+            float cand_norm;
+            const floatx16 acc = mfma_tile(cur, cand_norm);
+            hits_queue(cur, acc, cand_norm);
+            bump(3, nq > 0 ? (unsigned long long)cur.count * kQB : 0ull);
+            if (more) tile_store(t + 1);
+            __syncthreads();
+        }
+    } else if constexpr (BF) {
         bump(0, (unsigned long long)nq * a.N);
         if (qvalid) q_vend = 0x7fffffff;
         append_runs(0, lane == 0 ? a.N : 0);
@@ -971,7 +1070,7 @@ void search_kernel(SearchArgs a) {
             x_n = c % res0;
             row_n = c - x_n;
         }
-        lds_sync();
+        lsync();
         int nrows = 1;
         for (int d = 1; d < G; ++d) nrows *= 3;
         const float keep = 0.9999847412109375f;   // 1 - 2^-16
@@ -1037,7 +1136,7 @@ void search_kernel(SearchArgs a) {
                         s_rc[d] = d > 0 ? (R / s_stride[d]) % s_res[d] : 0;
                     }
                 }
-                lds_sync();
+                lsync();
 
                 if constexpr (counting) {
                     // the reference's shell candidates of this segment's queries:
@@ -1131,7 +1230,7 @@ void search_kernel(SearchArgs a) {
         }
     }
 
-    lds_sync();
+    lsync();
     {
         // the last partial batch, then the final selection of every list
         // (one call site for both keeps a single inlined copy of the sorts)
@@ -1141,7 +1240,7 @@ void search_kernel(SearchArgs a) {
     }
 
     if constexpr (counting) {
-        lds_sync();
+        lsync();
         if (lane < 5 && (lane != 4 || s_ctr[4] != 0)) atomicAdd(&a.counters[lane], s_ctr[lane]);
     }
 }
@@ -1152,12 +1251,18 @@ static unsigned f32_bits(float f) {
     return u;
 }
 
+// Waves per workgroup of brute force on wide rows (the waves share each
+// candidate tile through LDS); every other path runs one-wave workgroups.
+constexpr int kBFWaves = 4;
+
 template <int DS, bool REV, bool BF>
 static void launch_one(const SearchArgs& a, hipStream_t s) {
+    constexpr int NW = (BF && DS >= 64) ? kBFWaves : 1;
+    const dim3 grid((a.nchunks + NW - 1) / NW), block(kWave * NW);
     if (a.counters)
-        hipLaunchKernelGGL((search_kernel<DS, REV, BF, true>), dim3(a.nchunks), dim3(kWave), 0, s, a);
+        hipLaunchKernelGGL((search_kernel<DS, REV, BF, true, NW>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((search_kernel<DS, REV, BF, false>), dim3(a.nchunks), dim3(kWave), 0, s, a);
+        hipLaunchKernelGGL((search_kernel<DS, REV, BF, false, NW>), grid, block, 0, s, a);
 }
 
 template <int DS>
