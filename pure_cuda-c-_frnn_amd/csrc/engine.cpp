@@ -297,7 +297,10 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
     const long long cells = b.cells;
     const void* frame = b.frame;
     float* const frows = b.frows;
-    ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)Mq * cap, "allocating candidate lists"));
+    // brute force on wide rows may split the points into ranges, each with
+    // its own lists (merged into the first Mq rows)
+    const int ranges = frnn::search_ranges(plan, dim, b.N, Mq);
+    ST_TRY(grow(&e->lists, &e->lists_bytes, (size_t)Mq * cap * ranges, "allocating candidate lists"));
     if (e->counting)
         ST_TRY(launch_status(frnn::launch_fill_i32((int*)e->counters, 2 * kCounterSlots, 0, s),
                              "clearing counters"));
@@ -346,7 +349,7 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
                                              grid ? e->cell_of : nullptr, grid ? e->start : nullptr, frame,
                                              b.N, dim, K, plan, e->lists, cap,
                                              e->counting ? e->counters : nullptr, e->status_dev, s,
-                                             sep ? &qs : nullptr),
+                                             sep ? &qs : nullptr, ranges),
                          "search launch"));
     ST_TRY(mark_stage(e, 7));
     // stage 7: results to the original query order (ScatterToOrigKernel)

@@ -164,10 +164,16 @@ struct QuerySet {
     int M;
 };
 // queries == nullptr: every point is a query (the all-points search).
+// ranges: brute force on wide rows may split the points into that many
+// ranges (search_ranges), whose per-range lists lie at rows r * M + query of
+// `lists` (ranges * M rows) and are merged into rows 0 .. M-1; 1 for callers
+// whose lists hold M rows.
 int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
                   const int* cell_of,
                   const int* start, const void* frame_ws, int N, int D, int K, const frnn_plan_t& plan,
                   unsigned long long* lists, int cap, unsigned long long* counters, unsigned* status,
-                  hipStream_t s, const QuerySet* queries = nullptr);
+                  hipStream_t s, const QuerySet* queries = nullptr, int ranges = 1);
+// Point ranges the engine gives brute force on wide rows (1 for other plans).
+int search_ranges(const frnn_plan_t& plan, int D, int N, int M);
 
 }  // namespace frnn

@@ -160,6 +160,10 @@ struct SearchArgs {
     float norm_scale;            // 1 - c_norm
     float thr_rel, thr_abs;      // filter threshold margin
     int nchunks;
+    // brute force on wide rows: the points split into `slices` ranges of
+    // slice_tiles 32-point tiles, one workgroup per (query block, range); range
+    // s writes its own lists at rows s * M + query (merged afterwards)
+    int slices, slice_tiles;
 };
 
 __device__ __forceinline__ float filter_threshold(float thr, const SearchArgs& a) {
@@ -320,7 +324,8 @@ void search_kernel(SearchArgs a) {
     // (waves of a multi-wave workgroup past the last chunk have no queries)
     const int nq = MW ? max(min(kQB, a.M - q0), 0) : min(kQB, a.M - q0);
     const bool qvalid = n < nq;
-    unsigned long long* const lists = a.lists + (size_t)(MW ? min(q0, a.M) : q0) * a.cap;
+    unsigned long long* const lists =
+        a.lists + ((size_t)(MW ? blockIdx.y : 0) * a.M + (size_t)(MW ? min(q0, a.M) : q0)) * a.cap;
 
     if constexpr (kQueryLds) {
         const float* src = a.qpts + (size_t)(q0 + (qvalid ? n : 0)) * DS + h * HD;
@@ -965,14 +970,16 @@ void search_kernel(SearchArgs a) {
         // t + 1 into registers before tile t's MFMA chain and stores it after
         // the tile's hits; one workgroup barrier per tile separates the two
         // buffers' uses.  The per-wave hit handling never uses the workgroup
-        // barrier, so every wave passes the same barriers (ntiles of them).
-        bump(0, (unsigned long long)nq * a.N);
+        // barrier, so every wave passes the same barriers (t1 - t0 of them).
         if (qvalid) q_vend = 0x7fffffff;
         constexpr int kRowF4 = DS / 4;                    // float4 per row
         constexpr int kPer = 32 * kRowF4 / (kWave * NW);  // float4 per thread and tile
         static_assert(32 * kRowF4 % (kWave * NW) == 0, "tile loads split evenly");
         const int tid = threadIdx.x;
-        const int ntiles = (a.N + 31) / 32;
+        // this workgroup's range of the points: tiles [t0, t1)
+        const int t0 = (int)blockIdx.y * a.slice_tiles;
+        const int t1 = min((a.N + 31) / 32, t0 + a.slice_tiles);
+        bump(0, (unsigned long long)nq * (unsigned long long)max(min(a.N, 32 * t1) - 32 * t0, 0));
         float4 pf[kPer];
         auto tile_load = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
@@ -991,11 +998,13 @@ void search_kernel(SearchArgs a) {
                 *reinterpret_cast<float4*>(buf + (f / kRowF4) * BRS + 4 * (f % kRowF4)) = pf[k];
             }
         };
-        tile_load(0);
-        tile_store(0);
+        if (t0 < t1) {
+            tile_load(t0);
+            tile_store(t0);
+        }
         __syncthreads();
-        for (int t = 0; t < ntiles; ++t) {
-            const bool more = t + 1 < ntiles;
+        for (int t = t0; t < t1; ++t) {
+            const bool more = t + 1 < t1;
             if (more) tile_load(t + 1);
             Tile cur;
             cur.v0 = 32 * t;
@@ -1255,10 +1264,52 @@ static unsigned f32_bits(float f) {
 // candidate tile through LDS); every other path runs one-wave workgroups.
 constexpr int kBFWaves = 4;
 
+// Merge after brute force split over point ranges: row q of range 0 gets the
+// K smallest keys of rows q of ranges 0..S-1.  Each of those holds its range's
+// K smallest keys, ascending, padded with (r2, -1) (larger than every key
+// within the radius), so their union holds the K smallest overall.  One wave
+// per query, one pairwise bitonic merge per range: C[i] = min(X[i], Y[P-1-i])
+// (P = 64 EK) is bitonic and holds the P smallest of both, and the
+// half-cleaners sort it.
+template <int EK>
+__global__ __launch_bounds__(256) void merge_ranges_kernel(unsigned long long* __restrict__ lists, int cap, int M,
+                                                           int K, int S) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int q = (int)blockIdx.x * 4 + (int)(threadIdx.x / kWave);
+    if (q >= M) return;
+    unsigned long long* L0 = lists + (size_t)q * cap;
+    unsigned long long x[EK];
+#pragma unroll
+    for (int e = 0; e < EK; ++e) {
+        const int i = e * kWave + lane;
+        x[e] = i < K ? L0[i] : ~0ull;
+    }
+    for (int r = 1; r < S; ++r) {
+        const unsigned long long* Lr = lists + ((size_t)r * M + q) * cap;
+        unsigned long long y[EK];
+#pragma unroll
+        for (int e = 0; e < EK; ++e) {
+            const int i = e * kWave + lane;
+            y[e] = i < K ? Lr[i] : ~0ull;
+        }
+#pragma unroll
+        for (int e = 0; e < EK; ++e) {
+            const unsigned long long rb = shfl_u64(y[EK - 1 - e], kWave - 1 - lane);
+            x[e] = x[e] < rb ? x[e] : rb;
+        }
+        wave_bitonic_merge_u64<EK>(x);
+    }
+#pragma unroll
+    for (int e = 0; e < EK; ++e) {
+        const int i = e * kWave + lane;
+        if (i < K) L0[i] = x[e];
+    }
+}
+
 template <int DS, bool REV, bool BF>
 static void launch_one(const SearchArgs& a, hipStream_t s) {
     constexpr int NW = (BF && DS >= 64) ? kBFWaves : 1;
-    const dim3 grid((a.nchunks + NW - 1) / NW), block(kWave * NW);
+    const dim3 grid((a.nchunks + NW - 1) / NW, NW > 1 ? a.slices : 1), block(kWave * NW);
     if (a.counters)
         hipLaunchKernelGGL((search_kernel<DS, REV, BF, true, NW>), grid, block, 0, s, a);
     else
@@ -1271,10 +1322,58 @@ static void launch_ds(const SearchArgs& a, bool bf, hipStream_t s) {
     else launch_one<DS, false, false>(a, s);
 }
 
+// Point ranges for brute force on wide rows.  Every (query block, range)
+// workgroup streams the same number of tiles, so the kernel runs in whole
+// rounds of the device's resident workgroups; with too few blocks for the last
+// round, most of the device idles through it.  Splitting the points into S
+// ranges gives S times as many shorter workgroups: S is the smallest count
+// (at most 8) whose last round is at least 90% full, else the fullest.
+static int resident_bf_blocks(int DS) {
+    static int cached[2] = {0, 0};
+    const int k = DS >= 128 ? 1 : 0;
+    if (cached[k] > 0) return cached[k];
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    hipError_t e = DS >= 128
+        ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, search_kernel<128, false, true, false, kBFWaves>,
+                                                       kWave * kBFWaves, 0)
+        : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, search_kernel<64, false, true, false, kBFWaves>,
+                                                       kWave * kBFWaves, 0);
+    if (e != hipSuccess || per < 1) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    cached[k] = cus * per;
+    return cached[k];
+}
+
+int search_ranges(const frnn_plan_t& plan, int D, int N, int M) {
+    if (plan.path != FRNN_PATH_BRUTEFORCE || aos_stride(D) < 64 || N <= 0 || M <= 0) return 1;
+    const long long slots = resident_bf_blocks(aos_stride(D));
+    if (slots <= 0) return 1;
+    const long long blocks = ((long long)(M + kQB - 1) / kQB + kBFWaves - 1) / kBFWaves;
+    const int tiles = (N + 31) / 32;
+    int best = 1;
+    double best_fill = 0.0;
+    for (int S = 1; S <= 8 && S <= tiles; ++S) {
+        const long long units = blocks * S;
+        const long long rounds = (units + slots - 1) / slots;
+        const double fill = (double)units / (double)(rounds * slots);
+        if (fill >= 0.9) return S;
+        if (fill > best_fill + 1e-9) {
+            best_fill = fill;
+            best = S;
+        }
+    }
+    return best;
+}
+
 int launch_search(const float* aos, const float* frows, const void* stats_ws, const int* sorted_idx,
                   const int* cell_of, const int* start, const void* frame_ws, int N, int D, int K,
                   const frnn_plan_t& plan, unsigned long long* lists, int cap, unsigned long long* counters,
-                  unsigned* status, hipStream_t s, const QuerySet* queries) {
+                  unsigned* status, hipStream_t s, const QuerySet* queries, int ranges) {
     if (N <= 0) return 0;
     const bool bf = plan.path == FRNN_PATH_BRUTEFORCE;
     const QuerySet self{aos, frows, sorted_idx, cell_of, N};
@@ -1334,6 +1433,9 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     a.thr_rel = (float)(2.0 * (DS + 8.0) * u);
     a.thr_abs = 1.0e-35f;
     a.nchunks = (Q.M + kQB - 1) / kQB;
+    // point ranges (brute force on wide rows only)
+    a.slices = (bf && DS >= 64) ? max(1, min(ranges, 8)) : 1;
+    a.slice_tiles = ((N + 31) / 32 + a.slices - 1) / a.slices;
     if (plan.rev_order && !bf && DS == 4) {
         launch_one<4, true, false>(a, s);
     } else {
@@ -1347,6 +1449,13 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
             case 128: launch_ds<128>(a, bf, s); break;
             default: return 1;
         }
+    }
+    if (a.slices > 1) {
+        const int rc = launch_result();
+        if (rc != 0) return rc;
+        const dim3 mgrid((Q.M + 3) / 4), mblock(256);
+        if (K <= kWave) hipLaunchKernelGGL(merge_ranges_kernel<1>, mgrid, mblock, 0, s, lists, cap, Q.M, K, a.slices);
+        else hipLaunchKernelGGL(merge_ranges_kernel<2>, mgrid, mblock, 0, s, lists, cap, Q.M, K, a.slices);
     }
     return launch_result();
 }
