@@ -392,13 +392,20 @@ __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts,
     }
     const long long i0 = (long long)blockIdx.x * tile_stride;
     const int cnt = (int)max(0LL, min(256LL, (long long)N - i0));
-    for (int t = 0; t < T; ++t) {
-        float y = 0.0f;
-        if (tid < cnt) {
-            y = pts[(size_t)f->coord[t] * N + i0 + tid] - f->mean[t];
-            if (!(fabsf(y) <= 3.4e38f)) y = 0.0f;
+    {
+        // all of this thread's term loads in flight before the first is used
+        float x[kMaxTerms];
+#pragma unroll
+        for (int t = 0; t < kMaxTerms; ++t)
+            x[t] = (t < T && tid < cnt) ? pts[(size_t)f->coord[t] * N + i0 + tid] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < kMaxTerms; ++t) {
+            if (t < T) {
+                float y = tid < cnt ? x[t] - f->mean[t] : 0.0f;
+                if (!(fabsf(y) <= 3.4e38f)) y = 0.0f;
+                s_y[tid * kStride + t] = y;
+            }
         }
-        s_y[tid * kStride + t] = y;
     }
     __syncthreads();
     double acc[3] = {0.0, 0.0, 0.0};
@@ -447,15 +454,21 @@ __global__ __launch_bounds__(256) void cov_reduce_kernel(const double* __restric
     if (tid == 0) covsum[p] = s_sum[0];
 }
 
-// Wave sum / max of a double through the lane exchanges (no LDS).
+// Wave sum of a double that is 0 on lanes 32..63 (a frame has at most 32
+// terms, one per lane): five lane-exchange steps over lanes 0..31, then lane
+// 0's total to every lane (the same value the full six-step butterfly gives).
 __device__ __forceinline__ double wave_sum_f64(double v) {
+    static_assert(kMaxTerms <= 32, "terms live in lanes 0..31");
 #pragma unroll
-    for (int lj = 0; lj < 6; ++lj) {
+    for (int lj = 0; lj < 5; ++lj) {
         unsigned long long a, b;
         xor_pair_u64((unsigned long long)__double_as_longlong(v), 1 << lj, a, b);
         v = __longlong_as_double((long long)a) + __longlong_as_double((long long)b);
     }
-    return v;
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)u);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(u >> 32));
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
 }
 
 constexpr int kMaxDirs = FRNN_FRAME_DIRS;
@@ -526,7 +539,8 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     __shared__ double s_C[kMaxTerms][kMaxTerms + 1];   // covariance
     __shared__ double s_A[kMaxTerms][kMaxTerms + 1];   // (C / cmax)^2
     __shared__ double s_P[kMaxTerms][kMaxTerms + 1];   // C / cmax, then (C / cmax)^4
-    __shared__ double s_v[kMaxDirs][kMaxTerms];
+    __shared__ double s_v[kMaxDirs][kMaxTerms];          // directions
+    __shared__ double s_w[kMaxDirs][kMaxTerms];          // their product with a matrix
     const int t = threadIdx.x;
     const int T = f->terms;
     const int g = f->g;
@@ -559,105 +573,104 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     for (int k = 0; k < T; ++k) cmax = fmax(cmax, s_C[k][k]);
     const double cs = (cmax > 0.0 && cmax < 1.0e300) ? 1.0 / cmax : 1.0;
     if (on)
+#pragma unroll 1
         for (int k = 0; k < kMaxTerms; ++k) s_P[t][k] = s_C[t][k] * cs;
     lds_fence();
+    // Every lane takes NC entries of one row: 4 lanes x 4 columns per row for
+    // T <= 16, 2 lanes x 16 columns for T <= 32 (entries outside T x T stay
+    // 0).  Each entry sums over l in order, as a one-lane-per-row product would.
+    auto square_cols = [&](auto nc_const, double (*src)[kMaxTerms + 1], double (*dst)[kMaxTerms + 1]) {
+        constexpr int NC = decltype(nc_const)::value;
+        constexpr int R = NC == 4 ? 16 : 32;   // rows covered by the wave
+        const int row = t % R;
+        const int c0 = (t / R) * NC;
+        double acc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[c] = 0.0;
+        for (int l = 0; l < T; ++l) {
+            const double a = src[row][l];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[c] = fma(a, src[l][c0 + c], acc[c]);
+        }
+        lds_fence();
+#pragma unroll
+        for (int c = 0; c < NC; ++c) dst[row][c0 + c] = (row < T && c0 + c < T) ? acc[c] : 0.0;
+        lds_fence();
+    };
     auto square = [&](double (*src)[kMaxTerms + 1], double (*dst)[kMaxTerms + 1]) {
-        double acc[kMaxTerms];
-#pragma unroll
-        for (int k = 0; k < kMaxTerms; ++k) acc[k] = 0.0;
-        if (on) {
-            for (int l = 0; l < T; ++l) {
-                const double a = src[t][l];
-#pragma unroll
-                for (int k = 0; k < kMaxTerms; ++k) acc[k] = fma(a, src[l][k], acc[k]);
-            }
-        }
-        lds_fence();
-        if (on) {
-#pragma unroll
-            for (int k = 0; k < kMaxTerms; ++k) dst[t][k] = (k < T) ? acc[k] : 0.0;
-        }
-        lds_fence();
+        if (T <= 16) square_cols(IntC<4>{}, src, dst);
+        else square_cols(IntC<16>{}, src, dst);
     };
     square(s_P, s_A);
     square(s_A, s_P);
     square(s_P, s_A);   // s_A = (C / cmax)^8
-    double v[kMaxDirs];
-#pragma unroll
+    // The directions live in LDS (s_v[j][k]: component k of direction j;
+    // s_w: a product M v), lane t < kMaxTerms owning component t, and every
+    // loop below stays rolled: this one-wave kernel runs each instruction a
+    // few times at most, so its time goes to fetching code, which a compact
+    // body keeps short.
+    const int tc = t < kMaxTerms ? t : 0;   // lanes >= kMaxTerms read lane 0's slot, store nothing
     for (int j = 0; j < kMaxDirs; ++j)
-        v[j] = (on && j < m) ? ((t == j) ? 1.0 : 0.0625 * (double)((t * (2 * j + 3)) % 7 - 3)) : 0.0;
-    // modified Gram-Schmidt; a collapsed vector is replaced by the first
-    // coordinate direction with a substantial residual (one exists: j < m <= T)
+        if (t < kMaxTerms) s_v[j][t] = (on && j < m) ? ((t == j) ? 1.0 : 0.0625 * (double)((t * (2 * j + 3)) % 7 - 3)) : 0.0;
+    lds_fence();
+    // w_j = M v_j (M = C or its scaled eighth power): lane (r, j0) forms row r
+    // of directions j0 and j0 + 2, summing over k in order
+    auto matvec = [&](double (*M)[kMaxTerms + 1]) {
+        const int r = t & 31;
+        for (int j = t >> 5; j < m; j += 2) {
+            double w = 0.0;
+            for (int k = 0; k < T; ++k) w = fma(M[r][k], s_v[j][k], w);
+            s_w[j][r] = r < T ? w : 0.0;
+        }
+        lds_fence();
+    };
+    // modified Gram-Schmidt of s_w into s_v; a collapsed vector is replaced by
+    // the first coordinate direction with a substantial residual (one exists:
+    // j < m <= T).  Lanes >= kMaxTerms carry 0, as the wave sums require.
     auto orthonormalise = [&]() {
-#pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j) {
-            if (j >= m) break;
-            const double n_in = sqrt(wave_sum_f64(v[j] * v[j]));
-#pragma unroll
-            for (int k = 0; k < kMaxDirs; ++k)
-                if (k < j) v[j] -= wave_sum_f64(v[j] * v[k]) * v[k];
-            double nrm = sqrt(wave_sum_f64(v[j] * v[j]));
+        for (int j = 0; j < m; ++j) {
+            double x = t < kMaxTerms ? s_w[j][tc] : 0.0;
+            const double n_in = sqrt(wave_sum_f64(x * x));
+            for (int k = 0; k < j; ++k) {
+                const double vk = t < kMaxTerms ? s_v[k][tc] : 0.0;
+                x -= wave_sum_f64(x * vk) * vk;
+            }
+            double nrm = sqrt(wave_sum_f64(x * x));
             if (!(nrm > 1.0e-300 && nrm > 1.0e-12 * n_in && nrm < 1.0e300)) {
                 for (int c = 0; c < T; ++c) {
                     double cand = (t == c) ? 1.0 : 0.0;
-#pragma unroll
-                    for (int k = 0; k < kMaxDirs; ++k)
-                        if (k < j) cand -= wave_sum_f64(cand * v[k]) * v[k];
+                    for (int k = 0; k < j; ++k) {
+                        const double vk = t < kMaxTerms ? s_v[k][tc] : 0.0;
+                        cand -= wave_sum_f64(cand * vk) * vk;
+                    }
                     const double nc = sqrt(wave_sum_f64(cand * cand));
                     if (nc > 0.1) {
-                        v[j] = cand;
+                        x = cand;
                         nrm = nc;
                         break;
                     }
                 }
             }
-            v[j] /= nrm;
+            if (t < kMaxTerms) s_v[j][t] = x / nrm;
+            lds_fence();
         }
     };
-    // w_j = M v_j for all directions (M = C or its scaled fourth power), from
-    // one LDS broadcast of the iterate
-    auto matvec = [&](double (*M)[kMaxTerms + 1], double (&w)[kMaxDirs]) {
-#pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j)
-            if (on && j < m) s_v[j][t] = v[j];
-        lds_fence();
-#pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j) w[j] = 0.0;
-        for (int k = 0; k < T; ++k) {
-            const double c = M[on ? t : 0][k];
-#pragma unroll
-            for (int j = 0; j < kMaxDirs; ++j)
-                if (j < m) w[j] = fma(c, s_v[j][k], w[j]);
-        }
-        lds_fence();
-#pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j)
-            if (!on) w[j] = 0.0;
-    };
-    orthonormalise();
+    // (the start vectors are independent; the first product needs no
+    // orthonormal start)
     for (int it = 0; it < 2; ++it) {
-        double w[kMaxDirs];
-        matvec(s_A, w);
-#pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j) v[j] = w[j];
+        matvec(s_A);
         orthonormalise();
     }
     // Orthogonal iteration leaves direction j converged towards eigenvector j
     // (descending eigenvalues); its variance is the Rayleigh quotient v_j' C v_j.
     // A rotation inside the subspace would not change the captured variance.
-    double lam[kMaxDirs];
-    {
-        double w[kMaxDirs];
-        matvec(s_C, w);
-#pragma unroll
-        for (int j = 0; j < kMaxDirs; ++j) lam[j] = (j < m) ? wave_sum_f64(v[j] * w[j]) : 0.0;
-    }
+    matvec(s_C);
     constexpr double kShrink = 1.0 - 3.814697265625e-06;   // 1 - 2^-18
-#pragma unroll
-    for (int j = 0; j < kMaxDirs; ++j) {
-        if (j >= m) break;
-        if (on) f->dir[j][t] = (float)(v[j] * kShrink);
-        if (t == 0) f->sigma[j] = (float)sqrt(fmax(lam[j], 0.0));
+    for (int j = 0; j < m; ++j) {
+        const double x = t < kMaxTerms ? s_v[j][tc] : 0.0;
+        const double lam = wave_sum_f64(x * (t < kMaxTerms ? s_w[j][tc] : 0.0));
+        if (on) f->dir[j][t] = (float)(x * kShrink);
+        if (t == 0) f->sigma[j] = (float)sqrt(fmax(lam, 0.0));
     }
     if (t != 0) return;
     // ---- geometry (one thread) ----

@@ -8,6 +8,10 @@
 
 namespace frnn {
 
+// A compile-time int as a value (selects a template instance from a lambda).
+template <int V>
+struct IntC { static constexpr int value = V; };
+
 constexpr int kWave = 64;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));

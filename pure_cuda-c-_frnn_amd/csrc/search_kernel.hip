@@ -55,9 +55,6 @@ constexpr int kBatch = 64;                   // exact re-evaluations per batch
 constexpr int kQueueCap = kBatch + 16 * kWave;  // leftover batch + one tile's hits
 static_assert(FRNN_MAX_K + 128 <= 4 * kWave, "a candidate list fits the largest register sort");
 
-template <int V>
-struct IntC { static constexpr int value = V; };
-
 // Workgroups are one wave, so lanes only need their LDS accesses ordered: an
 // LDS-only fence around the barrier leaves outstanding global loads (the
 // prefetched tile) in flight, where __syncthreads() would wait for them.
