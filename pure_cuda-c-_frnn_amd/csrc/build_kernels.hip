@@ -408,14 +408,29 @@ __global__ __launch_bounds__(256) void cov_kernel(const float* __restrict__ pts,
         }
     }
     __syncthreads();
+    // eight interleaved partial sums per pair (point j goes to sum (j / slices)
+    // mod 8), added in a fixed order: eight LDS read pairs in flight per step
     double acc[3] = {0.0, 0.0, 0.0};
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         if (k < np) {
-            double sum = 0.0;
-            for (int j = slice; j < cnt; j += slices)
-                sum = fma((double)s_y[j * kStride + pa[k]], (double)s_y[j * kStride + pb[k]], sum);
-            acc[k] = sum;
+            const float* ya = s_y + pa[k];
+            const float* yb = s_y + pb[k];
+            double sum[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+            int j = slice;
+            for (; j + 7 * slices < cnt; j += 8 * slices) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int r = (j + u * slices) * kStride;
+                    sum[u] = fma((double)ya[r], (double)yb[r], sum[u]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 7; ++u) {
+                const int jj = j + u * slices;
+                if (jj < cnt) sum[u] = fma((double)ya[jj * kStride], (double)yb[jj * kStride], sum[u]);
+            }
+            acc[k] = ((sum[0] + sum[1]) + (sum[2] + sum[3])) + ((sum[4] + sum[5]) + (sum[6] + sum[7]));
         }
     }
     double* out = part + (size_t)blockIdx.x * kMaxPairs;
