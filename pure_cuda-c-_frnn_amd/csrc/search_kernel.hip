@@ -223,7 +223,6 @@ void search_kernel(SearchArgs a) {
     constexpr bool MW = NW > 1;
     static_assert(!MW || (BF && DS >= 64), "shared candidate tiles: brute force on wide rows");
     constexpr int HD = DS / 2;
-    constexpr bool PREFETCH = DS <= 32;
     // The chunk's query rows: staged in LDS for DS <= 32; wider rows are read
     // from the AoS array (the same 32 rows, cache resident), which keeps LDS
     // small enough for two workgroups per SIMD.  LDS rows are RS floats apart:
@@ -906,8 +905,13 @@ void search_kernel(SearchArgs a) {
     };
 
     // Stream the available candidates: each tile's MFMA chain is issued first,
-    // then (PREFETCH) the next tile's rows are gathered, so those loads are in
-    // flight while the MFMAs run and the current tile's hits are handled.
+    // then the next tile's rows are gathered, so those loads are in flight
+    // while the MFMAs run and the current tile's hits are handled.  Every row
+    // width takes this order.  (Gathering the next tile only after the
+    // consumed runs retire gave rows missing some neighbours at 64- and
+    // 128-float rows, although the same index arithmetic checks out on the
+    // CPU and adding a check of every gathered position made the misses
+    // vanish; that order is not used.)
     auto consume = [&](bool final_pass) __attribute__((always_inline)) {
         int avail = v_total - v_done;
         if (!(avail >= 32 || (final_pass && avail > 0))) return;
@@ -920,20 +924,14 @@ void search_kernel(SearchArgs a) {
             float cand_norm;
             const floatx16 acc = mfma_tile(cur, cand_norm);
             Tile nxt;
-            if constexpr (PREFETCH) {
-                if (has_next) gather(vn, min(32, an), nxt);
-            }
+            if (has_next) gather(vn, min(32, an), nxt);
             if constexpr (kTileExact) hits_tile_exact(cur, acc, cand_norm);
             else hits_queue(cur, acc, cand_norm);
             bump(3, (unsigned long long)cur.count * kQB);
             v_done = vn;
             while (ring_tail < ring_head && r_vend[ring_tail & (kRing - 1)] <= v_done) ++ring_tail;
             if (!has_next) break;
-            if constexpr (PREFETCH) {
-                cur = nxt;
-            } else {
-                gather(vn, min(32, an), cur);
-            }
+            cur = nxt;
         }
     };
 

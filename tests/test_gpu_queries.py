@@ -226,3 +226,17 @@ def test_queries_outside_the_points_range_on_a_projected_frame(D, k, N, r):
     assert_rows_equal(gi, gd, ri, rd, f"outside D={D}")
     for j, p in enumerate(far):
         assert (p in gi[j]) == (j % 4 < 2)
+
+
+@pytest.mark.parametrize("D,N,r,K", [(64, 20000, 0.2, 32), (128, 12000, 0.2, 64)])
+def test_queries_on_wide_row_grids(D, N, r, K):
+    # first-coordinate grids with 64- and 128-float rows: the queries' own
+    # centred filter rows, binned and reordered on the points' grid
+    X = unit_cloud(N, D, 4, 9)
+    Q = separate_queries(X, 3000, 6)
+    assert O.plan(N, D, K, r)["path"] == "grid_first"
+    log(f"queries on a wide-row grid: N={N} M={len(Q)} D={D} K={K} r={r}")
+    gi, gd, plan = engine_search_queries(X, Q, K, r)
+    assert plan["path"] == "grid_first"
+    ri, rd = O.search_queries(X, Q, K, r)
+    assert_rows_equal(gi, gd, ri, rd, f"queries wide grid D={D}")

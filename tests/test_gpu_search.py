@@ -354,3 +354,26 @@ def test_concurrent_calls_on_one_engine_are_serialised():
         t.join()
     eng.close()
     assert not errors, errors[0]
+
+
+WIDE_GRIDS = [
+    # label, D, N, radius, K: first-coordinate grids whose padded rows are 64 or
+    # 128 floats (centred filter rows, queued exact rechecks, the tile loop
+    # without the next-tile prefetch)
+    ("first_d40", 40, 20000, 0.2, 16),
+    ("first_d64", 64, 20000, 0.2, 32),
+    ("first_d100", 100, 20000, 0.2, 16),
+    ("first_d128", 128, 12000, 0.2, 64),
+]
+
+
+@pytest.mark.parametrize("label,D,N,r,K", WIDE_GRIDS)
+def test_wide_rows_on_grids(label, D, N, r, K):
+    X = unit_cloud(N, D, 4, 9)
+    X[11] = X[5]
+    assert O.plan(N, D, K, r)["path"] == "grid_first"
+    log(f"wide grid {label}: N={N} D={D} K={K} r={r}")
+    gi, gd, plan = engine_search(X, K, r)
+    assert plan["path"] == "grid_first"
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, label)
