@@ -538,9 +538,16 @@ __global__ __launch_bounds__(64) void raw_frame_kernel(int g, float cell_raw, fl
 // directions stay orthonormal up to a shrink (|U d| <= |d| for any d) and
 // every direction has norm < 1.
 //
-// Grid geometry: origin -4 sigma per axis, cell edge
+// Grid geometry: res_d = max(1, floor(8 sigma_d / h)) cells of edge
 //   h >= r (1 + 2^-12) + 2 margin + 2 slack,  slack = 2^-18 (4 sigma_max + h0),
-// enlarged until prod res <= cells_cap.  Two points within the radius (fp32
+// per axis, h enlarged until prod res <= cells_cap, and an axis of two or
+// more cells centred on the mean (origin -res h / 2, |origin| <= 4 sigma).
+// Rounding the count down and centring keep the end layers of thin axes from
+// holding a distribution tail next to a dense layer: chunks of such a sparse
+// layer span many rows, each query then streaming dense neighbouring rows
+// alone (one such layer of 1% of the points made a search 3.5x slower).
+// Points beyond the cells clamp into the edge cells, which every pruning test
+// treats as unbounded outward.  Two points within the radius (fp32
 // distance < r2, so |p - q| <= r (1 + 2^-15)) have computed projections closer
 // than r (1 + 2^-15) + 2 margin; with the rounding of the binning (bounded by
 // slack) their cell coordinates differ by at most one, so every neighbour lies
@@ -718,7 +725,7 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
         if (pass > 0) h *= 1.0625;
         cells = 1;
         for (int d = 0; d < kFrameGrid; ++d) {
-            double rd = d < g ? ceil(8.0 * sig[d] / h) : 1.0;
+            double rd = d < g ? floor(8.0 * sig[d] / h) : 1.0;
             rd = fmin(fmax(rd, 1.0), 1048576.0);
             res[d] = (int)rd;
             cells *= res[d];
@@ -743,7 +750,10 @@ __global__ __launch_bounds__(64) void frame_dirs_kernel(const double* __restrict
     int stride = 1;
     for (int d = 0; d < kFrameGrid; ++d) {
         f->res[d] = res[d];
-        f->lo[d] = d < g ? (float)(-4.0 * sig[d]) : 0.0f;
+        // a split axis is centred on the mean (res h <= 8 sigma, so |lo| <= 4 sigma);
+        // an axis of one cell bins everything to it whatever its origin
+        const int coarse = d == 0 && g >= 1 ? res[0] / fine0 : res[d];
+        f->lo[d] = d < g ? (float)(coarse >= 2 ? -0.5 * (double)coarse * (double)hf : -4.0 * sig[d]) : 0.0f;
         f->stride[d] = stride;
         stride *= res[d];
     }

@@ -63,6 +63,12 @@ __device__ __forceinline__ void lds_sync() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
+// Frames walk each segment's rows in two passes: the first at the inner
+// threshold inner_frac2(K) r^2 (or the segment's threshold if smaller), the
+// second at the segment's threshold as the first pass's candidates have
+// tightened it, streaming only what the first pass has not.
+constexpr int kPasses = 2;
+constexpr float kK16Frac2 = 2.0f;   // K <= 16: one pass
 constexpr int kRing = 128;                   // pending candidate runs (<= 31 + 64 in use)
 constexpr int kMaxG = 9;
 
@@ -153,6 +159,7 @@ struct SearchArgs {
     int hist_on;                 // threshold histograms in use (r2 is not tiny)
     int exact_limit;             // a filtered list above this gets the exact compaction
     unsigned r2bits;             // bits(r2)
+    float inner2;                // the first pass's threshold on frames (>= r2: one pass)
     float r2, cell, radius;      // cell: raw-grid cell edge
     float norm_scale;            // 1 - c_norm
     float thr_rel, thr_abs;      // filter threshold margin
@@ -1110,6 +1117,9 @@ void search_kernel(SearchArgs a) {
         int ib = 0, NI = 0;
         int xa = 0, nx = 1;
         float thr_seg = 0.0f;
+        float thr_out = 0.0f;               // this batch's pass: stretches up to this threshold
+        float thr_done = -1.0f;             // ... beyond those of earlier passes (-1: none)
+        bool two = false;                   // the segment's rows are walked in kPasses passes
         bool seg_mine = false;              // this lane's query is in the current segment
         bool last = false;
         while (!last) {
@@ -1169,18 +1179,34 @@ void search_kernel(SearchArgs a) {
 
                 xa = max(xlo - 1, 0);
                 nx = fr ? 1 : min(xhi + 1, res0 - 1) - xa + 1;
-                NI = nx * nrows;
+                two = fr && a.inner2 < a.r2;
+                NI = two ? kWave * (kPasses - 1) + 2 * nrows : nx * nrows;
+                thr_done = -1.0f;
                 ib = 0;
             }
             if (ib < NI) {
                 // the segment's largest threshold, as tightened by the
                 // compactions so far (nothing beyond it can still be accepted)
                 thr_seg = wave_max_f32(seg_mine ? key_d2(s_thr[n]) : -__builtin_huge_valf());
+                // passes: batch p (items p kWave + ...) is pass p; pass 0
+                // takes one item per row, later passes two: the parts of the
+                // row's stretch left (side 0) and right (side 1) of what the
+                // earlier passes streamed
+                const int pass = ib / kWave;
+                if (two) thr_out = pass < kPasses - 1 ? fminf(thr_seg, a.inner2) : thr_seg;
                 const int item = ib + lane;
+                int rowi = item / nx, side = 0;
+                bool valid = item < NI;
+                if (two) {
+                    const int j = item - pass * kWave;
+                    rowi = pass == 0 ? j : j >> 1;
+                    side = pass == 0 ? 0 : j & 1;
+                    valid = rowi < nrows;
+                }
                 int rs = 0, rl = 0;
-                if (item < NI) {
+                if (valid) {
                     const int x = xa + item % nx;
-                    int tt = natural_row(item / nx, G - 1), Rb = 0;
+                    int tt = natural_row(rowi, G - 1), Rb = 0;
                     bool ok = true;
                     float lb = 0.0f;     // squared gaps on axes 1..g-1
                     for (int d = 1; d < G; ++d) {
@@ -1203,16 +1229,41 @@ void search_kernel(SearchArgs a) {
                         // (w adds sqrt's rounding and slack + 2 margin); binning
                         // is monotone in the projection, so the stretch is the
                         // cell range of the window's ends (rounded outward).
-                        if (!(lb * keep > thr_seg)) {
-                            const float w2 = fmaxf(thr_seg * 1.0001220703125f - lb * keep, 0.0f);
+                        // Pass p streams the row's stretch at thr_out minus
+                        // the stretch at thr_done (the largest threshold of
+                        // the passes before it): stretches are monotone in the
+                        // threshold, so the passes together cover the stretch
+                        // at the segment's final-pass threshold, each
+                        // candidate once.
+                        auto stretch = [&](float thr, int& f0, int& f1) -> bool {
+                            if (lb * keep > thr) return false;
+                            const float w2 = fmaxf(thr * 1.0001220703125f - lb * keep, 0.0f);
                             const float w = sqrtf(w2) * 1.00000095367431640625f + gsm;
                             const float bl = s_blo[0], bh = s_bhi[0];
                             const float wl = (bl - w) - eps * (fabsf(bl) + w);
                             const float wh = (bh + w) + eps * (fabsf(bh) + w);
-                            const int fx0 = wl == wl ? sub_bin(wl, s_org[0], ginv0, res0) : 0;
-                            const int fx1 = wh == wh ? sub_bin(wh, s_org[0], ginv0, res0) : res0 - 1;
-                            rs = a.start[Rb + fx0];
-                            rl = max(a.start[Rb + fx1 + 1] - rs, 0);
+                            f0 = wl == wl ? sub_bin(wl, s_org[0], ginv0, res0) : 0;
+                            f1 = wh == wh ? sub_bin(wh, s_org[0], ginv0, res0) : res0 - 1;
+                            return true;
+                        };
+                        int f0 = 1, f1 = 0;
+                        if (!two || pass == 0) {
+                            if (!stretch(two ? thr_out : thr_seg, f0, f1)) f1 = f0 - 1;
+                        } else {
+                            int i0 = 0, i1 = 0;
+                            const bool inner = thr_done >= 0.0f && stretch(thr_done, i0, i1);
+                            if (!stretch(thr_out, f0, f1)) {
+                                f1 = f0 - 1;
+                            } else if (inner) {
+                                if (side == 0) f1 = min(f1, i0 - 1);
+                                else f0 = max(f0, i1 + 1);
+                            } else if (side == 1) {
+                                f1 = f0 - 1;
+                            }
+                        }
+                        if (f0 <= f1) {
+                            rs = a.start[Rb + f0];
+                            rl = max(a.start[Rb + f1 + 1] - rs, 0);
                         }
                     } else if (ok) {
                         const float gp = axis_gap(0, x);
@@ -1227,6 +1278,7 @@ void search_kernel(SearchArgs a) {
                     }
                 }
                 append_runs(rs, rl);
+                if (two) thr_done = fmaxf(thr_done, thr_out);
                 ib += kWave;
             }
             last = ib >= NI && seg >= nq;
@@ -1247,6 +1299,17 @@ void search_kernel(SearchArgs a) {
         lsync();
         if (lane < 5 && (lane != 4 || s_ctr[4] != 0)) atomicAdd(&a.counters[lane], s_ctr[lane]);
     }
+}
+
+// The first pass's threshold as a fraction of r^2, by K: the inner ball
+// should hold about K points, so that pass sets thresholds near the K-th
+// distance.  Measured on the BASELINE configs (ms per call, one pass /
+// fraction 0.06 / 0.16): metric (K=64) 3.89 / 3.74 / 3.71, C4 (K=64)
+// 6.91 / 6.33 / 6.26, C3 (K=32) 1.80 / 1.34 / 1.43, C2 (K=32) 1.61 / 1.46 /
+// 1.50, C1 (K=16) 0.30 / 0.31 / 0.31.
+static float inner_frac2(int K) {
+    if (K <= 16) return kK16Frac2;
+    return K <= 32 ? 0.06f : 0.16f;
 }
 
 static unsigned f32_bits(float f) {
@@ -1417,6 +1480,7 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
         }
     }
     a.r2 = plan.r2;
+    a.inner2 = inner_frac2(K) * plan.r2;
     const int DS = aos_stride(D);
     a.cell = bf ? 1.0f : plan.cell_size;
     a.radius = plan.cell_size;

@@ -277,7 +277,7 @@ def test_frame_grid(name, N):
     u = 2.0 ** -24
     assert (T + 2) * u * R <= fi.margin <= 1.01 * (T + 2) * u * R
     # geometry: cell edge >= r (1 + 2^-12) + 2 margin + 2 slack, binning
-    # reciprocal rounded down, origins at -4 sigma, grid within the capacity;
+    # reciprocal rounded down, grid within the capacity;
     # axis 0 split into fine0 cells of edge h / fine0 (exact scalings)
     r = float(np.float32(w.radius))
     h0 = r * (1 + 2.0 ** -12) + 2 * fi.margin
@@ -290,8 +290,13 @@ def test_frame_grid(name, N):
     assert res[0] % F == 0
     assert np.all(res >= 1) and fi.cells == np.prod(res) <= cap
     assert list(fi.stride[:g]) == [int(np.prod(res[:d])) for d in range(g)]
+    # cells per axis: max(1, floor(8 sigma / h)); split axes centred on the mean
     for d in range(g):
-        assert fi.lo[d] == np.float32(-4.0 * np.float64(fi.sigma[d]))
+        coarse = fi.res[d] // (F if d == 0 else 1)
+        m = max(1, int(np.floor(8.0 * np.float64(fi.sigma[d]) / np.float64(fi.h))))
+        assert coarse in (m, m + 1)      # the kernel divides by h before its fp32 round-up
+        if coarse >= 2:
+            assert fi.lo[d] == np.float32(-0.5 * coarse * np.float64(np.float32(fi.h)))
     # binning, recomputed in exact fp32
     S = _project(w.X, fi, slots)
     cc = np.stack([_sub_bins(S[d], fi.lo[d], fi.inv_h0 if d == 0 else fi.inv_h, fi.res[d]) for d in range(g)], 1)
