@@ -81,20 +81,21 @@ constexpr int kMaxG = 9;
 // up to b hold at least K keys of the list, the K-th smallest key lies below
 // bucket b's upper edge, so no key at or above it can be among the K results:
 // the query's threshold drops to that edge without sorting the list.  Buckets
-// are a quarter octave of d2 wide (S = 21) and reach 4 octaves below r2.
-// Counts are bytes, four to a word (a list never holds more than 255 keys).
+// are 2^S fp32 ulps of d2 wide: S = 21 (a quarter octave, the buckets reach 4
+// octaves below r2) for K <= 32, S = 20 (an eighth, 2 octaves) for larger K,
+// whose K-th distance lies nearer the radius; hist_shift picks S.  Counts are
+// bytes, four to a word (a list never holds more than 255 keys).
 constexpr int kHB = 16;                      // buckets per query
-constexpr int kHS = 21;                      // bucket width: 2^21 fp32 ulps of d2
 constexpr int kHW = kHB / 4;                 // histogram words per query
 constexpr int kMaxRoom = 255;                // list entries in use (byte counts)
 
-__device__ __forceinline__ int hist_bucket(float d2, unsigned top) {
-    const unsigned u = (top - 1u - __float_as_uint(d2)) >> kHS;
+__device__ __forceinline__ int hist_bucket(float d2, unsigned top, int hs) {
+    const unsigned u = (top - 1u - __float_as_uint(d2)) >> hs;
     return kHB - 1 - (int)min(u, (unsigned)(kHB - 1));
 }
 // key just above bucket b: a key is below it iff its d2 lies in a bucket <= b
-__device__ __forceinline__ unsigned long long hist_edge_key(int b, unsigned top) {
-    return (unsigned long long)(top - ((unsigned)(kHB - 1 - b) << kHS)) << 32;
+__device__ __forceinline__ unsigned long long hist_edge_key(int b, unsigned top, int hs) {
+    return (unsigned long long)(top - ((unsigned)(kHB - 1 - b) << hs)) << 32;
 }
 
 // Traversal order of a segment's 3^m neighbouring rows (m = g - 1 axes): by
@@ -159,6 +160,7 @@ struct SearchArgs {
     int hist_on;                 // threshold histograms in use (r2 is not tiny)
     int exact_limit;             // a filtered list above this gets the exact compaction
     unsigned r2bits;             // bits(r2)
+    int hist_shift;              // histogram bucket width: 2^hist_shift ulps of d2
     float inner2;                // the first pass's threshold on frames (>= r2: one pass)
     float r2, cell, radius;      // cell: raw-grid cell edge
     float norm_scale;            // 1 - c_norm
@@ -444,7 +446,7 @@ void search_kernel(SearchArgs a) {
     auto end_round = [&](bool acc, int qn, unsigned long long key) __attribute__((always_inline)) {
         const bool any = __ballot(acc) != 0;
         if (a.hist_on && any && acc) {
-            const int b = hist_bucket(key_d2(key), a.r2bits);
+            const int b = hist_bucket(key_d2(key), a.r2bits, a.hist_shift);
             atomicAdd(&s_hist[qn * kHW + (b >> 2)], 1u << (8 * (b & 3)));
             atomicAdd(&s_hcle[qn], 1);
         }
@@ -462,7 +464,7 @@ void search_kernel(SearchArgs a) {
                     cb = hb[b];
                 }
                 if (b != b0) {
-                    const unsigned long long ek = hist_edge_key(b, a.r2bits);
+                    const unsigned long long ek = hist_edge_key(b, a.r2bits, a.hist_shift);
                     const unsigned long long t = s_thr[n];
                     const unsigned long long nt = ek < t ? ek : t;
                     thr_f = filter_threshold(key_d2(nt), a);
@@ -562,13 +564,13 @@ void search_kernel(SearchArgs a) {
                 for (int e = 0; e < EK; ++e) {
                     const int i = e * kWave + lane;
                     if (i < keep) {
-                        const int b = hist_bucket(key_d2(x[e]), a.r2bits);
+                        const int b = hist_bucket(key_d2(x[e]), a.r2bits, a.hist_shift);
                         atomicAdd(&s_hist[qn * kHW + (b >> 2)], 1u << (8 * (b & 3)));
                     }
                 }
                 if (lane == 0) {
                     s_hcle[qn] = keep;
-                    s_hb[qn] = (unsigned char)(c >= a.K ? hist_bucket(key_d2(kth), a.r2bits) : kHB - 1);
+                    s_hb[qn] = (unsigned char)(c >= a.K ? hist_bucket(key_d2(kth), a.r2bits, a.hist_shift) : kHB - 1);
                 }
             }
         }
@@ -1470,7 +1472,8 @@ int launch_search(const float* aos, const float* frows, const void* stats_ws, co
     // (at K <= 16 the lists rarely fill, and the histogram upkeep after every
     // exact round costs more than its tighter thresholds save: C1 0.30 ->
     // 0.28 ms, the reference's K=16 sweep cells 3-4% faster without it)
-    a.hist_on = (K > 16 && a.r2bits >= ((unsigned)kHB << kHS)) ? 1 : 0;
+    a.hist_shift = K <= 32 ? 21 : 20;
+    a.hist_on = (K > 16 && a.r2bits >= ((unsigned)kHB << a.hist_shift)) ? 1 : 0;
     a.exact_limit = (K + a.room - kBatch) / 2;
     a.G = bf ? 0 : plan.grid_dim;
     a.res = bf ? 1 : plan.res;
