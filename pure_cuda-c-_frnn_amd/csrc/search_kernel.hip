@@ -259,7 +259,7 @@ void search_kernel(SearchArgs a) {
     // (query, sorted position) and re-evaluate them 64 at a time from memory.
     constexpr bool kTileExact = DS <= 32;
     __shared__ unsigned char s_qn_w[kTileExact ? 1 : NW * kQueueCap];
-    __shared__ int s_qpos_w[kTileExact ? 1 : NW * kQueueCap];
+    __shared__ __align__(8) int s_qpos_w[kTileExact ? 1 : NW * kQueueCap];
     // candidate run ring: [start, start + (vend - vbeg)) of the sorted points
     // at virtual stream positions [vbeg, vend).  Runs are contiguous in the
     // stream, so a run's vbeg is the vend of the run before it (slot
@@ -277,7 +277,11 @@ void search_kernel(SearchArgs a) {
     __shared__ __align__(16) float t_rows[kTileExact ? 32 * TS : 4];
     // (a tile holds at most 32 x 32 hits; 64 more entries take the writes of
     // lanes without a hit, one per lane)
-    __shared__ unsigned short s_hit[kTileExact ? 32 * 32 + kWave : 2];
+    __shared__ __align__(8) unsigned short s_hit[kTileExact ? 32 * 32 + kWave : 2];
+    // The final selection compacts a list into up to 128 keys of LDS: the hit
+    // entries (tile-exact path) or the wave's queue slice, both idle by then.
+    static_assert(sizeof(unsigned short) * (32 * 32 + kWave) >= 128 * 8 && sizeof(int) * kQueueCap >= 128 * 8,
+                  "final selection staging");
     // grid geometry per axis (cells, cell-id stride, origin), the segment's
     // bounding box and row coordinates, and each query's grid coordinates
     __shared__ int s_res[kMaxG], s_stride[kMaxG];
@@ -306,6 +310,8 @@ void search_kernel(SearchArgs a) {
     unsigned char* const s_qn = s_qn_w + (kTileExact ? 0 : wave * kQueueCap);
     int* const s_qpos = s_qpos_w + (kTileExact ? 0 : wave * kQueueCap);
     int* const t_pos = t_pos_w + (kTileExact ? 0 : wave * 32);
+    unsigned long long* const s_fin =
+        kTileExact ? reinterpret_cast<unsigned long long*>(s_hit) : reinterpret_cast<unsigned long long*>(s_qpos);
     // Synchronisation of a wave's own LDS traffic.  A one-wave workgroup uses
     // the barrier with LDS-only fences; in a multi-wave workgroup the per-wave
     // code (hits, lists, selection) must not use the workgroup barrier (its
@@ -607,7 +613,74 @@ void search_kernel(SearchArgs a) {
         lsync();
         return base;
     };
+    // Final selection of query qn's list for K <= 64 (one sort register).  The
+    // keys at or below the query's threshold, a superset of its K smallest,
+    // are compacted into LDS in list order.  Up to 64 of them take one
+    // register sort.  Up to 128 fill a second register x1 that is brought into
+    // descending order, so that min(x0[i], x1[i]) is bitonic and holds the 64
+    // smallest of both, which the half-cleaners sort: a second register of at
+    // most 16 keys sits in lanes 48..63, where the first four levels of the
+    // network (blocks of 16, lanes with bit 4 set descending) already sort it
+    // descending behind the ~0 fill; a fuller one is sorted and reversed.
+    // Returns false, having changed nothing, when more than 128 keys lie at
+    // or below the threshold (the general path then runs).
+    auto final_small = [&](int qn) __attribute__((always_inline)) -> bool {
+        unsigned long long* L = lists + (size_t)qn * a.cap;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        const int c = min(s_cnt[qn], a.room);
+        const unsigned long long thr = s_thr[qn];
+        // the whole list in one round trip (c <= 255 < 4 * 64)
+        unsigned long long v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = e * kWave + lane;
+            v[e] = (i < c) ? L[i] : ~0ull;
+        }
+        int cnt = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = e * kWave + lane;
+            const bool kp = i < c && v[e] <= thr;
+            const unsigned long long mk = __ballot(kp);
+            const int pos = cnt + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(mk >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((unsigned)mk, 0u));
+            if (kp && pos < 2 * kWave) s_fin[pos] = v[e];
+            cnt += __popcll(mk);
+        }
+        if (cnt > 2 * kWave) return false;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront", "local");
+        unsigned long long x0[1];
+        x0[0] = lane < cnt ? s_fin[lane] : ~0ull;
+        if (cnt > kWave) {
+            const int w = cnt - kWave;
+            unsigned long long x1[1];
+            if (w <= 16) {
+                x1[0] = lane >= kWave - 16 && lane - (kWave - 16) < w ? s_fin[lane + 16] : ~0ull;
+                wave_sort_u64<1>(x0);
+#pragma unroll
+                for (int lk = 1; lk <= 4; ++lk) {
+#pragma unroll
+                    for (int lj = lk - 1; lj >= 0; --lj) bitonic_step<1>(x1, 1 << lk, 1 << lj);
+                }
+            } else {
+                x1[0] = lane < w ? s_fin[kWave + lane] : ~0ull;
+                wave_sort_u64<1>(x0);
+                wave_sort_u64<1>(x1);
+                x1[0] = shfl_u64(x1[0], kWave - 1 - lane);
+            }
+            x0[0] = x0[0] < x1[0] ? x0[0] : x1[0];
+            wave_bitonic_merge_u64<1>(x0);
+        } else {
+            wave_sort_u64<1>(x0);
+        }
+        if (lane < a.K) L[lane] = lane < cnt ? x0[0] : make_key(a.r2, -1);
+        lsync();
+        return true;
+    };
     auto select_topk = [&](int qn, bool final_pass) __attribute__((always_inline)) {
+        // (lists whose new keys fit one register take the general path: the
+        // same single sort without the staging)
+        if (final_pass && a.K <= kWave && min(s_cnt[qn], a.room) - s_srt[qn] > kWave && final_small(qn)) return;
         // a final list with stale keys beyond two sort registers is filtered
         // first (a smaller sort)
         if (final_pass && a.hist_on && min(s_cnt[qn], a.room) - s_srt[qn] > 2 * kWave) filter_list(qn);
@@ -1051,12 +1124,17 @@ void search_kernel(SearchArgs a) {
         const Frame* fr = a.frame;
         const bool proj = fr != nullptr && fr->projected != 0;
         const int G = a.G;
-        const int res0 = fr ? fr->res[0] : a.res;
-        const float gh = fr ? fr->h : a.cell;
-        const float gh0 = fr ? fr->h0 : a.cell;
-        const float ginv0 = fr ? fr->inv_h0 : 0.0f;
-        const int fine0 = fr ? fr->fine0 : 1;
-        const float gsm = fr ? fr->slack + 2.0f * fr->margin : 0.0f;
+        // (wave-uniform values, kept in scalar registers)
+        auto su = [](int v) __attribute__((always_inline)) { return __builtin_amdgcn_readfirstlane(v); };
+        auto sf = [](float v) __attribute__((always_inline)) {
+            return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+        };
+        const int res0 = su(fr ? fr->res[0] : a.res);
+        const float gh = sf(fr ? fr->h : a.cell);
+        const float gh0 = sf(fr ? fr->h0 : a.cell);
+        const float ginv0 = sf(fr ? fr->inv_h0 : 0.0f);
+        const int fine0 = su(fr ? fr->fine0 : 1);
+        const float gsm = sf(fr ? fr->slack + 2.0f * fr->margin : 0.0f);
         if (lane < G) {
             s_res[lane] = fr ? fr->res[lane] : a.res;
             s_stride[lane] = fr ? fr->stride[lane] : a.gstride[lane];
