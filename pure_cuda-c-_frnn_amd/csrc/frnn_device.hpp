@@ -77,6 +77,16 @@ __device__ __forceinline__ float key_d2(unsigned long long key) {
 //   j = 16    v_permlane16_swap (rows 0/1 and 2/3 of a and b hold each other)
 //   j = 32    v_permlane32_swap (the two 32-lane halves)
 // j must fold to a constant (loops over it are fully unrolled).
+// Lane masks as compile-time constants: bit i of kLaneBitClear[l] is set iff
+// bit l of lane i is clear.  Selections by these masks stay scalar constants
+// the compiler can rematerialise; masks computed from the lane id are not
+// constant to it and would each hold a scalar register pair for the whole
+// kernel.
+constexpr unsigned long long kLaneBitClear[6] = {
+    0x5555555555555555ull, 0x3333333333333333ull, 0x0F0F0F0F0F0F0F0Full,
+    0x00FF00FF00FF00FFull, 0x0000FFFF0000FFFFull, 0x00000000FFFFFFFFull};
+__device__ __forceinline__ bool lane_mask(unsigned long long m) { return __builtin_amdgcn_inverse_ballot_w64(m); }
+
 __device__ __forceinline__ void xor_pair_u32(unsigned v, int j, unsigned& a, unsigned& b) {
     switch (j) {
         case 1: a = v; b = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true); return;
@@ -85,7 +95,7 @@ __device__ __forceinline__ void xor_pair_u32(unsigned v, int j, unsigned& a, uns
             const unsigned dn = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true);  // lane - 4
             const unsigned up = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x12C, 0xF, 0xF, true);  // lane + 4
             a = v;
-            b = (threadIdx.x & 4) ? dn : up;
+            b = lane_mask(kLaneBitClear[2]) ? up : dn;
             return;
         }
         case 8: a = v; b = (unsigned)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true); return;
@@ -124,7 +134,6 @@ __device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int
 // bit k of the element index is clear (k = 0: ascending everywhere).
 template <int E>
 __device__ __forceinline__ void bitonic_step(unsigned long long (&x)[E], int k, int j) {
-    const int lane = threadIdx.x & (kWave - 1);
     if (j >= kWave) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -142,9 +151,14 @@ __device__ __forceinline__ void bitonic_step(unsigned long long (&x)[E], int k, 
         for (int e = 0; e < E; ++e) {
             unsigned long long p, q;
             xor_pair_u64(x[e], j, p, q);
-            const bool up = (((e * kWave) | lane) & k) == 0;
-            const bool keep_min = ((lane & j) == 0) == up;
-            x[e] = ((p < q) == keep_min) ? p : q;
+            // lanes ascending: bit k of the element index clear (k < 64: a
+            // lane bit; otherwise the register's, the same for all lanes)
+            const unsigned long long up = k == 0 ? ~0ull
+                                          : k < kWave ? kLaneBitClear[__builtin_ctz(k)]
+                                                      : (((e * kWave) & k) == 0 ? ~0ull : 0ull);
+            // a lane keeps the minimum iff (its bit j is clear) == ascending
+            const unsigned long long keep_min = ~(kLaneBitClear[__builtin_ctz(j)] ^ up);
+            x[e] = ((p < q) == lane_mask(keep_min)) ? p : q;
         }
     }
 }

@@ -275,12 +275,11 @@ void search_kernel(SearchArgs a) {
     __shared__ int t_pos_w[kTileExact ? 1 : NW * 32];
     __shared__ int t_idx[kTileExact ? 32 : 1];
     __shared__ __align__(16) float t_rows[kTileExact ? 32 * TS : 4];
-    // (a tile holds at most 32 x 32 hits; 64 more entries take the writes of
-    // lanes without a hit, one per lane)
-    __shared__ __align__(8) unsigned short s_hit[kTileExact ? 32 * 32 + kWave : 2];
+    // (a tile holds at most 32 x 32 hits)
+    __shared__ __align__(8) unsigned short s_hit[kTileExact ? 32 * 32 : 2];
     // The final selection compacts a list into up to 128 keys of LDS: the hit
     // entries (tile-exact path) or the wave's queue slice, both idle by then.
-    static_assert(sizeof(unsigned short) * (32 * 32 + kWave) >= 128 * 8 && sizeof(int) * kQueueCap >= 128 * 8,
+    static_assert(sizeof(unsigned short) * 32 * 32 >= 128 * 8 && sizeof(int) * kQueueCap >= 128 * 8,
                   "final selection staging");
     // grid geometry per axis (cells, cell-id stride, origin), the segment's
     // bounding box and row coordinates, and each query's grid coordinates
@@ -881,14 +880,19 @@ void search_kernel(SearchArgs a) {
         const bool fast = __ballot(!whole) == 0;
         const bool take = width != 0;
         int total = 0;
-        // every lane writes (no branch): a hit at its ballot prefix offset,
-        // a non-hit to its own slot past the hit entries.  m is the mask of
-        // the register's hits (each condition a single compare, combined in
-        // scalar registers).
+        // m is the mask of register r's hits (each condition a single
+        // compare, combined in scalar registers).  Most registers of a tile
+        // with hits have none (about 60% at the headline workload): those
+        // skip on a scalar test; otherwise the hit lanes write their entries
+        // at the ballot prefix offsets past `total` (the running count is the
+        // mbcnt accumulator).
         auto push = [&](int r, unsigned long long m) __attribute__((always_inline)) {
-            const bool hr = __builtin_amdgcn_inverse_ballot_w64(m);
-            const int pre = (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
-            s_hit[hr ? total + pre : 32 * 32 + lane] = (unsigned short)(((8 * (r >> 2) + (r & 3)) << 5) + lane_code);
+            if (m == 0) return;
+            if (__builtin_amdgcn_inverse_ballot_w64(m)) {
+                const int pos = (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((unsigned)m, (unsigned)total));
+                s_hit[pos] = (unsigned short)(((8 * (r >> 2) + (r & 3)) << 5) + lane_code);
+            }
             total += __popcll(m);
         };
         if (fast) {
