@@ -86,6 +86,9 @@ constexpr unsigned long long kLaneBitClear[6] = {
     0x5555555555555555ull, 0x3333333333333333ull, 0x0F0F0F0F0F0F0F0Full,
     0x00FF00FF00FF00FFull, 0x0000FFFF0000FFFFull, 0x00000000FFFFFFFFull};
 __device__ __forceinline__ bool lane_mask(unsigned long long m) { return __builtin_amdgcn_inverse_ballot_w64(m); }
+// lane < 32 (the lower half of the wave) and lane == 0, in the same form
+__device__ __forceinline__ bool lower_half() { return lane_mask(0x00000000FFFFFFFFull); }
+__device__ __forceinline__ bool first_lane() { return lane_mask(1ull); }
 
 __device__ __forceinline__ void xor_pair_u32(unsigned v, int j, unsigned& a, unsigned& b) {
     switch (j) {
@@ -197,7 +200,9 @@ __device__ __forceinline__ unsigned wave_reduce_u32(unsigned v, Op op) {
     xor_pair_u32(v, 4, p, q); v = op(p, q);
     xor_pair_u32(v, 2, p, q); v = op(p, q);
     xor_pair_u32(v, 1, p, q); v = op(p, q);
-    return v;
+    // every lane holds the result: as a scalar, it keeps the control flow
+    // that depends on it uniform
+    return (unsigned)__builtin_amdgcn_readfirstlane((int)v);
 }
 __device__ __forceinline__ int wave_min_i32(int v) {
     return (int)wave_reduce_u32((unsigned)v, [](unsigned p, unsigned q) { return (unsigned)min((int)p, (int)q); });
@@ -223,7 +228,9 @@ __device__ __forceinline__ long long wave_sum_i64(long long v) {
     xor_pair_u64(x, 4, p, q); x = p + q;
     xor_pair_u64(x, 2, p, q); x = p + q;
     xor_pair_u64(x, 1, p, q); x = p + q;
-    return (long long)x;
+    const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)x);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(x >> 32));
+    return (long long)(((unsigned long long)hi << 32) | lo);
 }
 
 }  // namespace frnn

@@ -351,7 +351,7 @@ void search_kernel(SearchArgs a) {
     // row of query qn (a valid query of the chunk; queue path, wide rows)
     auto query_row = [&](int qn) -> const float* { return a.qpts + (size_t)(q0 + qn) * DS; };
     if (CNT && lane < 5) s_ctr[lane] = 0;
-    if (lane < kQB) {
+    if (lower_half()) {
         s_cnt[lane] = 0;
         s_srt[lane] = 0;
         s_thr[lane] = make_key(a.r2, 0);
@@ -360,7 +360,7 @@ void search_kernel(SearchArgs a) {
     }
 #pragma unroll
     for (int i = lane; i < kQB * kHW; i += kWave) s_hist[i] = 0u;
-    if (lane == 0 && wave == 0) r_vend[kRing - 1] = 0;
+    if (first_lane() && wave == 0) r_vend[kRing - 1] = 0;
     lsync();
     // Filter operands are the rows centred on the input mean, fl(x - mean).
     // Rows of up to 32 floats are centred in registers as they are loaded
@@ -404,7 +404,7 @@ void search_kernel(SearchArgs a) {
         unsigned pa, pb;
         xor_pair_u32(__float_as_uint(pn), 32, pa, pb);
         qn2 = __uint_as_float(pa) + __uint_as_float(pb);
-        bop[HD] = (h == 0) ? a.norm_scale : qn2 * a.norm_scale;
+        bop[HD] = lower_half() ? a.norm_scale : qn2 * a.norm_scale;
     }
     if (!qvalid) {
 #pragma unroll
@@ -420,13 +420,13 @@ void search_kernel(SearchArgs a) {
     // (query, candidate) pairs, list/queue capacity overflows.
     constexpr bool counting = CNT;
     auto bump = [&](int i, unsigned long long v) __attribute__((always_inline)) {
-        if (counting && lane == 0) s_ctr[i] += v;
+        if (counting && first_lane()) s_ctr[i] += v;
     };
     // A capacity guard fired (a logic error): the caller's status word says so
     // (wave-uniform call).
     auto report_overflow = [&](bool ovf) __attribute__((always_inline)) {
         if (counting) bump(4, __popcll(__ballot(ovf)));
-        if (a.status && __ballot(ovf) != 0 && lane == 0) a.status[0] = 1u;
+        if (a.status && __ballot(ovf) != 0 && first_lane()) a.status[0] = 1u;
     };
     int q_size = 0;                     // queue entries (wave-uniform)
 
@@ -473,7 +473,7 @@ void search_kernel(SearchArgs a) {
                     const unsigned long long t = s_thr[n];
                     const unsigned long long nt = ek < t ? ek : t;
                     thr_f = filter_threshold(key_d2(nt), a);
-                    if (h == 0) {
+                    if (lower_half()) {
                         s_hb[n] = (unsigned char)b;
                         s_hcle[n] = cle;
                         s_thr[n] = nt;
@@ -553,9 +553,9 @@ void search_kernel(SearchArgs a) {
                 for (int e = 1; e < EK; ++e)
                     if (e == ek) kth = x[e];
                 kth = shfl_u64(kth, (a.K - 1) & (kWave - 1));
-                if (lane == 0) s_thr[qn] = kth;
+                if (first_lane()) s_thr[qn] = kth;
             }
-            if (lane == 0) {
+            if (first_lane()) {
                 s_cnt[qn] = keep;
                 s_srt[qn] = keep;
             }
@@ -573,7 +573,7 @@ void search_kernel(SearchArgs a) {
                         atomicAdd(&s_hist[qn * kHW + (b >> 2)], 1u << (8 * (b & 3)));
                     }
                 }
-                if (lane == 0) {
+                if (first_lane()) {
                     s_hcle[qn] = keep;
                     s_hb[qn] = (unsigned char)(c >= a.K ? hist_bucket(key_d2(kth), a.r2bits, a.hist_shift) : kHB - 1);
                 }
@@ -605,7 +605,7 @@ void search_kernel(SearchArgs a) {
             nm += __popcll(__ballot(kp && i < m));
             base += __popcll(mk);
         }
-        if (lane == 0) {
+        if (first_lane()) {
             s_cnt[qn] = base;
             s_srt[qn] = nm;
         }
@@ -706,7 +706,7 @@ void search_kernel(SearchArgs a) {
     // Before a round: compact every list that could overflow during it, then
     // reload the filter thresholds.
     auto make_room = [&]() __attribute__((always_inline)) {
-        const bool need = (lane < kQB) && s_cnt[lane] > a.room - kBatch;
+        const bool need = lower_half() && s_cnt[lane] > a.room - kBatch;
         unsigned long long m = __ballot(need);
         if (m) {
             while (m) {
@@ -724,7 +724,7 @@ void search_kernel(SearchArgs a) {
     auto process_batch = [&](int base, int count, bool final_pass) __attribute__((always_inline)) {
         // (one call site of the selection for both uses keeps a single
         // inlined copy of the sorts)
-        const bool need = (lane < kQB) && (final_pass ? lane < nq : s_cnt[lane] > a.room - kBatch);
+        const bool need = lower_half() && (final_pass ? lane < nq : s_cnt[lane] > a.room - kBatch);
         unsigned long long m = __ballot(need);
         if (m) {
             while (m) {
@@ -817,7 +817,7 @@ void search_kernel(SearchArgs a) {
         xor_pair_u32(__float_as_uint(pn), 32, pa, pb);
         const float nrm = __uint_as_float(pa) + __uint_as_float(pb);
         cand_norm = nrm;
-        const float last = (h == 0) ? (n < t.count ? nrm : 3.0e38f) : 1.0f;
+        const float last = lower_half() ? (n < t.count ? nrm : 3.0e38f) : 1.0f;
         return __builtin_amdgcn_mfma_f32_32x32x2f32(last, bop[HD], acc, 0, 0, 0);
     };
 
@@ -951,7 +951,7 @@ void search_kernel(SearchArgs a) {
         }
         if (__ballot(gh[0] || gh[1] || gh[2] || gh[3]) == 0) return;
         lsync();
-        if (h == 0) t_pos[n] = t.pos;
+        if (lower_half()) t_pos[n] = t.pos;
         lsync();
         int first, width;
         rows_of(t.v0, t.count, first, width);
@@ -981,7 +981,7 @@ void search_kernel(SearchArgs a) {
                 }
             }
         }
-        if (q_size > kQueueCap && a.status && lane == 0) a.status[0] = 1u;
+        if (q_size > kQueueCap && a.status && first_lane()) a.status[0] = 1u;
         lsync();
         int qs = min(q_size, kQueueCap);
         while (qs >= kBatch) {
@@ -1015,7 +1015,9 @@ void search_kernel(SearchArgs a) {
             else hits_queue(cur, acc, cand_norm);
             bump(3, (unsigned long long)cur.count * kQB);
             v_done = vn;
-            while (ring_tail < ring_head && r_vend[ring_tail & (kRing - 1)] <= v_done) ++ring_tail;
+            while (ring_tail < ring_head &&
+                   __builtin_amdgcn_readfirstlane(r_vend[ring_tail & (kRing - 1)]) <= v_done)
+                ++ring_tail;
             if (!has_next) break;
             cur = nxt;
         }
@@ -1030,9 +1032,11 @@ void search_kernel(SearchArgs a) {
 #pragma unroll
         for (int o = 1; o < kWave; o <<= 1) {
             const int y = __shfl_up(incl, o);
-            if (lane >= o) incl += y;
+            if (lane_mask(~((1ull << o) - 1ull))) incl += y;
         }
-        const int total = __shfl(incl, kWave - 1);
+        // (the stream length is wave-uniform: kept in a scalar register, so
+        // the tile loop's control flow stays scalar)
+        const int total = __builtin_amdgcn_readfirstlane(__shfl(incl, kWave - 1));
         const int k = __popcll(mask & ((1ull << lane) - 1ull));
         if (has) {
             const int slot = (ring_head + k) & (kRing - 1);
@@ -1113,7 +1117,7 @@ void search_kernel(SearchArgs a) {
     } else if constexpr (BF) {
         bump(0, (unsigned long long)nq * a.N);
         if (qvalid) q_vend = 0x7fffffff;
-        append_runs(0, lane == 0 ? a.N : 0);
+        append_runs(0, first_lane() ? a.N : 0);
         consume(true);
     } else {
         // Grid geometry: a projected frame's axes (first-coordinate plans with
@@ -1149,12 +1153,12 @@ void search_kernel(SearchArgs a) {
         if (proj) {
             float sp[kFrameGrid];
             frame_project(fr, [&](int d) { return qrow[d]; }, sp);
-            if (h == 0) {
+            if (lower_half()) {
 #pragma unroll
                 for (int d = 0; d < kFrameGrid; ++d)
                     if (d < G) s_qg[n * kGA + d] = sp[d];
             }
-        } else if (h == 0) {
+        } else if (lower_half()) {
             for (int d = 0; d < G; ++d) s_qg[n * kGA + d] = qrow[d];
         }
         // the query's cell, as binned: x along axis 0, the row as the id of
@@ -1208,7 +1212,7 @@ void search_kernel(SearchArgs a) {
         bool last = false;
         while (!last) {
             if (ib >= NI && seg < nq) {
-                const int R = __shfl(row_n, seg);
+                const int R = __builtin_amdgcn_readlane(row_n, seg);
                 const bool in_seg = (row_n == R);
                 seg_mine = in_seg;
                 // the previous segment's stream ends here, this one's starts
@@ -1228,7 +1232,7 @@ void search_kernel(SearchArgs a) {
                     const float qd = s_qg[n * kGA + d];
                     const float lo = wave_min_f32(in_seg ? qd : __builtin_huge_valf());
                     const float hi = wave_max_f32(in_seg ? qd : -__builtin_huge_valf());
-                    if (lane == 0) {
+                    if (first_lane()) {
                         s_blo[d] = lo;
                         s_bhi[d] = hi;
                         s_rc[d] = d > 0 ? (R / s_stride[d]) % s_res[d] : 0;
@@ -1241,7 +1245,7 @@ void search_kernel(SearchArgs a) {
                     // the cells x-1..x+1 of edge h (fine0 axis-0 cells each) in
                     // the 3^(g-1) rows
                     long long sh = 0;
-                    if (in_seg && h == 0) {
+                    if (in_seg && lower_half()) {
                         const int xc = x_n / fine0;
                         const int f0 = max(xc - 1, 0) * fine0;
                         const int f1 = min((xc + 2) * fine0, res0) - 1;
