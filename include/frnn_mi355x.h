@@ -188,8 +188,11 @@ int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
 
 /* Profiling (replaces the reference's FRNN_REPORT_OCCUPANCY diagnostics,
  * find_nbrs.cu:355-382).  flags: FRNN_PROFILE_EVENTS records per-stage HIP
- * events; FRNN_PROFILE_COUNTERS runs the counting build of the search kernel
- * and reads its work counters back after each search (0: neither).  Stages:
+ * events; FRNN_PROFILE_SEARCH_EVENTS records only the two around the
+ * neighbour search (stage 6; the others read 0), which keeps the event
+ * overhead out of timed calls; FRNN_PROFILE_COUNTERS runs the counting build
+ * of the search kernel and reads its work counters back after each search
+ * (0: none).  Stages:
  * 0 zero-fill, 1 point statistics, 2 grid frame, 3 bin+count, 4 scan,
  * 5 reorder/transpose (and, for separate queries, their binning, scan and
  * reorder), 6 neighbour search, 7 unpermute.  After frnn_engine_query, stages
@@ -198,6 +201,7 @@ int frnn_engine_last_plan(const frnn_engine_t* engine, frnn_plan_t* out);
 #define FRNN_NUM_STAGES 8
 #define FRNN_PROFILE_EVENTS 1
 #define FRNN_PROFILE_COUNTERS 2
+#define FRNN_PROFILE_SEARCH_EVENTS 4
 int frnn_engine_set_profiling(frnn_engine_t* engine, int flags);
 int frnn_engine_stage_times(const frnn_engine_t* engine, float* ms, int n);
 /* Work counters of the last search run with FRNN_PROFILE_COUNTERS:

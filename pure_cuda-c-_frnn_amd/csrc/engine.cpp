@@ -145,6 +145,7 @@ struct frnn_engine {
     bool has_result = false;
     int last_N = 0, last_K = 0;
     bool profiling = false;   // per-stage HIP events
+    bool search_events = false;   // HIP events around the search kernel only
     bool counting = false;    // work counters (the counting search kernel)
     hipEvent_t ev[FRNN_NUM_STAGES + 1] = {};
     bool ev_recorded[FRNN_NUM_STAGES + 1] = {};   // recorded since the last build
@@ -176,7 +177,7 @@ void release(frnn_engine* e) {
 // Stage events: every call records the stages it runs; stage_times() reads
 // the ones of the last call that ran the search.
 int mark_stage(frnn_engine* e, int i) {
-    if (e->profiling) {
+    if (e->profiling || (e->search_events && (i == 6 || i == 7))) {
         HIP_TRY(hipEventRecord(e->ev[i], e->stream), "event record");
         e->ev_recorded[i] = true;
     }
@@ -309,6 +310,8 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
     // search order, or transposed for brute force; their filter rows are
     // centred on the points' mean, as the points' are
     frnn::QuerySet qs{};
+    // this call's search and unpermute stages record afresh
+    for (int i = 6; i <= FRNN_NUM_STAGES; ++i) e->ev_recorded[i] = false;
     if (own_prep) {
         for (int i = 0; i <= 5; ++i) e->ev_recorded[i] = false;
         ST_TRY(mark_stage(e, 5));
@@ -360,7 +363,7 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
     HIP_TRY(hipStreamSynchronize(s), "search pipeline");
     if (__atomic_load_n(e->status_host, __ATOMIC_SEQ_CST) != 0)
         return fail(FRNN_ERR_HIP, "internal list/queue capacity overflow in the search kernel");
-    if (e->profiling)
+    if (e->profiling || e->search_events)
         for (int i = 0; i < FRNN_NUM_STAGES; ++i) {
             // stages the build ran without profiling read as 0
             e->stage_ms[i] = 0.0f;
@@ -644,9 +647,10 @@ int frnn_engine_last_plan(const frnn_engine_t* e, frnn_plan_t* out) {
 
 int frnn_engine_set_profiling(frnn_engine_t* e, int flags) {
     if (!e) return fail(FRNN_ERR_INVALID_ARGUMENT, "null engine");
-    if (flags & ~(FRNN_PROFILE_EVENTS | FRNN_PROFILE_COUNTERS))
+    if (flags & ~(FRNN_PROFILE_EVENTS | FRNN_PROFILE_COUNTERS | FRNN_PROFILE_SEARCH_EVENTS))
         return fail(FRNN_ERR_INVALID_ARGUMENT, "unknown profiling flags");
     e->profiling = (flags & FRNN_PROFILE_EVENTS) != 0;
+    e->search_events = (flags & FRNN_PROFILE_SEARCH_EVENTS) != 0;
     e->counting = (flags & FRNN_PROFILE_COUNTERS) != 0;
     return FRNN_OK;
 }

@@ -33,7 +33,7 @@ MAX_DIM = 128
 MAX_CELLS = 1_000_000
 NUM_STAGES = 8
 NUM_COUNTERS = 4
-PROFILE_EVENTS, PROFILE_COUNTERS = 1, 2
+PROFILE_EVENTS, PROFILE_COUNTERS, PROFILE_SEARCH_EVENTS = 1, 2, 4
 STAGE_NAMES = ("zero_fill", "stats", "frame", "bin_count", "scan", "reorder", "search", "unpermute")
 PATH_NAMES = {-1: "empty", 0: "bruteforce", 1: "grid_full", 2: "grid_first"}
 
@@ -312,10 +312,13 @@ class FRNNEngine:
         return p.as_dict()
 
     @_serialised
-    def set_profiling(self, enable=True, counters=True):
+    def set_profiling(self, enable=True, counters=True, search_only=False):
         """enable: per-stage HIP event times (stage_times()); counters: also run
-        the counting build of the search kernel (counters())."""
-        flags = (PROFILE_EVENTS | (PROFILE_COUNTERS if counters else 0)) if enable else 0
+        the counting build of the search kernel (counters()); search_only:
+        events around the search kernel only (the other stages read 0), which
+        keeps the event overhead out of timed calls."""
+        ev = PROFILE_SEARCH_EVENTS if search_only else PROFILE_EVENTS
+        flags = (ev | (PROFILE_COUNTERS if counters else 0)) if enable else 0
         _check(_load().frnn_engine_set_profiling(self._handle(), flags), "set_profiling")
 
     @_serialised
