@@ -767,12 +767,40 @@ __global__ __launch_bounds__(256) void bin_frame_kernel(const float* __restrict_
                                                         const Frame* __restrict__ f, int cells,
                                                         int* __restrict__ cell_of, int* __restrict__ rank,
                                                         int* __restrict__ cnt) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    // the projection terms, staged once per block: each point's coordinate
+    // loads then issue together instead of one term's load waiting on the
+    // term's coordinate index
+    __shared__ int s_coord[kMaxTerms];
+    __shared__ float s_mean[kMaxTerms];
+    __shared__ float s_dir[kFrameGrid][kMaxTerms];
+    const int tid = threadIdx.x;
+    if (tid < kMaxTerms) {
+        s_coord[tid] = f->coord[tid];
+        s_mean[tid] = f->mean[tid];
+#pragma unroll
+        for (int m = 0; m < kFrameGrid; ++m) s_dir[m][tid] = f->dir[m][tid];
+    }
+    __syncthreads();
+    const int i = blockIdx.x * blockDim.x + tid;
     if (i >= N) return;
     const int g = f->g;
     float s[kFrameGrid];
     if (f->projected) {
-        frame_project(f, [&](int d) { return pts[(size_t)d * N + i]; }, s);
+        // frame_project's sums: the fma chain over the terms in order
+        const int T = f->terms;
+        float x[kMaxTerms];
+#pragma unroll
+        for (int t = 0; t < kMaxTerms; ++t) x[t] = t < T ? pts[(size_t)s_coord[t] * N + i] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < kFrameGrid; ++m) s[m] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kMaxTerms; ++t) {
+            if (t < T) {
+                const float y = x[t] - s_mean[t];
+#pragma unroll
+                for (int m = 0; m < kFrameGrid; ++m) s[m] = fmaf(s_dir[m][t], y, s[m]);
+            }
+        }
     } else {
 #pragma unroll
         for (int d = 0; d < kFrameGrid; ++d) s[d] = d < g ? pts[(size_t)d * N + i] : 0.0f;
