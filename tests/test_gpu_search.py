@@ -67,6 +67,36 @@ def test_duplicates_and_ties():
         assert_rows_equal(gi, gd, ri, rd, f"ties K={K}")
 
 
+# The final selection (K <= 64) takes one of four forms by the number of list
+# keys at or below the query's threshold: <= 64 (one sort register), 65-80 (a
+# second register of <= 16 keys sorted by the network's first four levels),
+# 81-128 (a second full register), > 128 (the general filter-and-merge path).
+# Clusters of exact duplicates put that many keys at d2 = 0 (all in the lowest
+# histogram bucket, ties broken by index) in every member's list, so each size
+# below lands in a chosen form; no list is compacted before the end (sizes <
+# 255 - 64).  Jittered copies beside them give distinct small distances.
+FINAL_SIZES = (40, 64, 66, 75, 80, 81, 100, 128, 129, 150, 180)
+
+
+@pytest.mark.parametrize("D,k,r", [(3, 3, 0.05), (16, 4, 0.2)])
+@pytest.mark.parametrize("K", [32, 48, 64])
+def test_final_selection_forms(D, k, r, K):
+    rs = np.random.RandomState(40 + D + K)
+    X = [unit_cloud(20000, D, k, 21)]
+    for j, size in enumerate(FINAL_SIZES):
+        c = X[0][rs.randint(0, 20000)]
+        dup = np.repeat(c[None, :], size, axis=0)
+        if j % 2:   # half of the clusters: jittered copies (distinct d2 far below r2)
+            dup = dup + (1e-4 * r) * rs.standard_normal(dup.shape).astype(np.float32)
+        X.append(dup.astype(np.float32))
+    X = np.concatenate(X)
+    log(f"final selection forms: N={len(X)} D={D} K={K} r={r} plan={O.plan(len(X), D, K, r)['path']}")
+    gi, gd, plan = engine_search(X, K, r)
+    assert plan["path"] != "bruteforce"
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, f"final forms D={D} K={K}")
+
+
 def test_out_of_domain_points_are_clamped_not_dropped():
     rs = np.random.RandomState(4)
     X = rs.uniform(-0.3, 1.3, (5000, 3)).astype(np.float32)
