@@ -265,6 +265,17 @@ def test_profiling_counters_and_stage_times():
     assert st["frame"] > 0
     assert c["shell_candidates"] >= c["accepted"]
     assert c["streamed_pairs"] >= c["filter_hits"] >= c["accepted"] > 0
+    # events around the search kernel only: every other stage reads 0, also
+    # after calls that recorded all of them
+    eng.set_profiling(True, counters=False, search_only=True)
+    for _ in range(2):
+        eng.search_gpu(d.data_ptr(), 20000, 16, 32, 0.15)
+        st = eng.stage_times()
+        assert st["search"] > 0
+        assert all(v == 0 for k, v in st.items() if k != "search"), st
+    gi, gd = eng.get_results_numpy(20000, 32)
+    ri, rd = O.search(X, 32, 0.15)
+    assert_rows_equal(gi.reshape(32, 20000).T, gd.reshape(32, 20000).T, ri, rd, "search-only events")
     eng.close()
 
 
