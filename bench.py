@@ -57,16 +57,18 @@ def eprint(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_bytes(N, D, ds, g, C, framed):
+def build_bytes(N, D, ds, g, C, framed, zero_filled):
     """Algorithmic HBM bytes of each build kernel (4-byte ints and floats); ds is
     the padded row length of the AoS rows the reorder writes, C the grid's cells
-    (a frame's capacity for framed plans)."""
+    (a frame's actual cells), zero_filled the count entries the build filled
+    (0 once a previous call's count scan has left the array zero)."""
     T = min(D, 32)
     b = {
-        "zero_fill": 4 * (C + 1),
+        "zero_fill": 4 * zero_filled,
         "stats": 4 * D * N,
         "bin_count": 4 * (T if framed else g) * N + 8 * N + 8 * (C + 1),
-        "scan": 8 * (C + 1),
+        # read the counts, write the offsets, zero the counts
+        "scan": 12 * (C + 1),
         "reorder": 20 * N + 4 * D * N + (8 if ds >= 64 else 4) * ds * N,
     }
     if framed:
@@ -252,6 +254,7 @@ def main():
         eng.search_gpu(ptr, w.N, w.D, w.K, w.radius)
         for k, v in eng.stage_times().items():
             stage_sum[k] = stage_sum.get(k, 0.0) + v
+    cwork = eng.count_work()
     eng.set_profiling(True, counters=True)
     eng.search_gpu(ptr, w.N, w.D, w.K, w.radius)
     ctr = eng.counters()
@@ -299,9 +302,8 @@ def main():
                     "shell_candidate_pairs": ctr["shell_candidates"]}
 
     if plan["path"] != "bruteforce":
-        bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"],
-                         frnn_cuda.grid_cells(w.N, w.D, w.K, w.radius),
-                         frnn_cuda.frame_workspace_bytes(w.N, w.D, w.K, w.radius) > 0)
+        bb = build_bytes(w.N, w.D, frnn_cuda.aos_stride(w.D), plan["grid_dim"], cwork["scanned"] - 1,
+                         frnn_cuda.frame_workspace_bytes(w.N, w.D, w.K, w.radius) > 0, cwork["zero_filled"])
     else:
         ds = frnn_cuda.aos_stride(w.D)
         bb = {"stats": 4 * w.D * w.N, "reorder": 4 * w.D * w.N + (8 if ds >= 64 else 4) * ds * w.N}
@@ -309,6 +311,8 @@ def main():
     tot_b, tot_ms = 0, 0.0
     for k, b in bb.items():
         ms = stages[k]
+        if b == 0:
+            continue    # a stage with no work this call (the count fill after the first)
         gbs = b / (ms / 1e3) / 1e9 if ms > 0 else 0.0
         build[k] = {"bytes": b, "ms": round(ms, 4), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         tot_b += b

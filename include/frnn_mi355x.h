@@ -213,6 +213,13 @@ int frnn_engine_stage_times(const frnn_engine_t* engine, float* ms, int n);
  * capacity guards ever fired. */
 #define FRNN_NUM_COUNTERS 4
 int frnn_engine_counters(const frnn_engine_t* engine, long long* out, int n);
+/* Count-array work of the last build (no reference counterpart: the figures
+ * behind the build's HBM accounting): out[0] = entries zero-filled (0 when
+ * the previous call's count scan had left the array zero), out[1] = entries
+ * the count scan covered (a frame's cells + 1, read back from the device
+ * only while FRNN_PROFILE_EVENTS is set; otherwise the plan's capacity + 1;
+ * 0 without a grid). */
+int frnn_engine_count_work(const frnn_engine_t* engine, long long* out, int n);
 
 /* ---- kernel launch seam (replaces run_*, frnn_engine.cu:9-20) ------------ */
 /* All pointers are device pointers; launches are asynchronous on `stream`. */

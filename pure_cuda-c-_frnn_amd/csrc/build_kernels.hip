@@ -108,10 +108,18 @@ __device__ __forceinline__ int block_exclusive_scan_256(int v, int* s_w, int* to
     return off + incl - v;
 }
 
+// bound (may be null): a device count; the scan then covers min(n, *bound +
+// 1) entries (the frame's cells + 1 of a count array sized for its capacity).
+__device__ __forceinline__ int scan_extent(int n, const int* bound) {
+    return bound ? min(n, __builtin_amdgcn_readfirstlane(bound[0]) + 1) : n;
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int* __restrict__ in, int n,
-                                                                   int* __restrict__ partials) {
+                                                                   int* __restrict__ partials,
+                                                                   const int* __restrict__ bound) {
     __shared__ int s_w[kScanThreads / kWave];
+    n = scan_extent(n, bound);
     const long long base = (long long)blockIdx.x * kScanTile + 4 * threadIdx.x;
     int sum = 0;
 #pragma unroll
@@ -145,15 +153,23 @@ __global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int* __rest
     }
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kScanThreads) void scan_final_kernel(const int* __restrict__ in, int n,
+// CLEAR: the input entries are zeroed once read (the count array starts the
+// next binning clean, with no separate fill).
+template <bool VEC, bool CLEAR>
+__global__ __launch_bounds__(kScanThreads) void scan_final_kernel(int* __restrict__ in, int n,
                                                                   const int* __restrict__ partials,
-                                                                  int* __restrict__ out) {
+                                                                  int* __restrict__ out,
+                                                                  const int* __restrict__ bound) {
     __shared__ int s_w[kScanThreads / kWave];
+    n = scan_extent(n, bound);
     const long long base = (long long)blockIdx.x * kScanTile + 4 * threadIdx.x;
     int4 v[kScanRows];
 #pragma unroll
     for (int j = 0; j < kScanRows; ++j) v[j] = scan_load4<VEC>(in, base + j * 4 * kScanThreads, n);
+    if constexpr (CLEAR) {
+#pragma unroll
+        for (int j = 0; j < kScanRows; ++j) scan_store4<VEC>(in, base + j * 4 * kScanThreads, n, make_int4(0, 0, 0, 0));
+    }
     int carry = partials[blockIdx.x];
 #pragma unroll
     for (int j = 0; j < kScanRows; ++j) {
@@ -1002,19 +1018,35 @@ int launch_exclusive_scan_noalloc(const int* in, int n, int* out, hipStream_t s)
 
 hipError_t scan_noalloc_error() { return g_scratch_err; }
 
-int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s) {
+namespace {
+template <bool CLEAR>
+int scan_launch(const int* in, int n, int* out, int* partials, const int* bound, hipStream_t s) {
     if (n <= 0) return 0;
     const int nb = (n + kScanTile - 1) / kScanTile;
     if (nb > kScanTile) return 2;
     const bool vec = (((uintptr_t)in | (uintptr_t)out) & 15) == 0;
-    if (vec) hipLaunchKernelGGL(scan_reduce_kernel<true>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials);
-    else hipLaunchKernelGGL(scan_reduce_kernel<false>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials);
+    int* const io = const_cast<int*>(in);   // written only with CLEAR
+    if (vec)
+        hipLaunchKernelGGL(scan_reduce_kernel<true>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, bound);
+    else
+        hipLaunchKernelGGL(scan_reduce_kernel<false>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, bound);
     hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partials, nb);
     if (vec)
-        hipLaunchKernelGGL(scan_final_kernel<true>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out);
+        hipLaunchKernelGGL((scan_final_kernel<true, CLEAR>), dim3(nb), dim3(kScanThreads), 0, s, io, n, partials,
+                           out, bound);
     else
-        hipLaunchKernelGGL(scan_final_kernel<false>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, out);
+        hipLaunchKernelGGL((scan_final_kernel<false, CLEAR>), dim3(nb), dim3(kScanThreads), 0, s, io, n,
+                           partials, out, bound);
     return launch_result();
+}
+}  // namespace
+
+int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s) {
+    return scan_launch<false>(in, n, out, partials, nullptr, s);
+}
+
+int launch_count_scan(int* cnt, int n, const int* bound, int* out, int* partials, hipStream_t s) {
+    return scan_launch<true>(cnt, n, out, partials, bound, s);
 }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }

@@ -106,6 +106,12 @@ struct frnn_engine {
     int* sorted_idx = nullptr;
     int* inv = nullptr;
     int* cnt = nullptr;
+    // leading entries of cnt known to be zero: a build fills only past them;
+    // the count scan zeroes what the binning wrote, so every call after the
+    // first skips the fill
+    long long cnt_zero = 0;
+    long long last_fill = 0;      // entries the last build zero-filled
+    long long last_scan = 0;      // entries its count scan covered (read back when profiling)
     int* start = nullptr;
     int* partials = nullptr;
     unsigned long long* counters = nullptr;
@@ -184,6 +190,37 @@ int mark_stage(frnn_engine* e, int i) {
     return FRNN_OK;
 }
 
+// Makes the first n count entries zero (a fill past the known-zero prefix)
+// and marks them dirty for the binning that follows.
+int clean_counts(frnn_engine* e, long long n) {
+    if (e->cnt_zero < n) {
+        ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, n, 0, e->stream), "zero-fill cells"));
+        e->last_fill = n;
+        e->cnt_zero = n;
+    }
+    e->cnt_zero = 0;   // until the count scan below has zeroed what binning wrote
+    return FRNN_OK;
+}
+
+// Exclusive scan of the counts into out, over the frame's cells + 1 when a
+// frame holds them (its cell count is on the device), else cells + 1; the
+// scan zeroes the counts it reads, and binning wrote no others.
+int count_scan(frnn_engine* e, long long cells, const void* frame, int* out) {
+    const int* bound = frame ? reinterpret_cast<const int*>(static_cast<const char*>(frame) +
+                                                            offsetof(frnn::Frame, cells))
+                             : nullptr;
+    ST_TRY(launch_status(frnn::launch_count_scan(e->cnt, (int)cells + 1, bound, out, e->partials, e->stream),
+                         "scan launch"));
+    e->cnt_zero = cells + 1;
+    e->last_scan = cells + 1;
+    if (bound && e->profiling)
+        HIP_TRY(hipMemcpyAsync(e->status_host + 4, bound, sizeof(int), hipMemcpyDeviceToHost, e->stream),
+                "reading the frame's cell count");
+    else
+        e->status_host[4] = (unsigned)cells;
+    return FRNN_OK;
+}
+
 // Stages 0-5 on the N points (SoA device input): plan, statistics, frame,
 // bin + count, scan, reorder (or the brute-force AoS copy).
 int build_points(frnn_engine* e, BuiltGrid& b, const float* d_pts, int N, int dim, int K, float radius) {
@@ -228,8 +265,11 @@ int build_points(frnn_engine* e, BuiltGrid& b, const float* d_pts, int N, int di
     }
     const void* const frame = b.frame;
     ST_TRY(mark_stage(e, 0));
-    // stage 0: zero-fill the counts (frnn_engine.cu:89-90)
-    if (grid) ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, cells + 1, 0, s), "zero-fill cells"));
+    // stage 0: zero-fill the counts (frnn_engine.cu:89-90), unless the last
+    // count scan left them zero
+    e->last_fill = 0;
+    e->last_scan = 0;
+    if (grid) ST_TRY(clean_counts(e, cells + 1));
     ST_TRY(mark_stage(e, 1));
     // stage 1: per-coordinate statistics (filter centre, frame terms)
     ST_TRY(launch_status(frnn::launch_point_stats(d_pts, N, dim, e->stats_ws, s), "statistics launch"));
@@ -246,9 +286,7 @@ int build_points(frnn_engine* e, BuiltGrid& b, const float* d_pts, int N, int di
                              "bin/count launch"));
     ST_TRY(mark_stage(e, 4));
     // stage 4: exclusive scan of the counts (thrust::exclusive_scan, frnn_engine.cu:91-94)
-    if (grid)
-        ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)cells + 1, e->start, e->partials, s),
-                             "scan launch"));
+    if (grid) ST_TRY(count_scan(e, cells, frame, e->start));
     ST_TRY(mark_stage(e, 5));
     // stage 5: reorder into cell order (CountingSort{ND,AoS3}Kernel) or, for
     // brute force, the AoS copy
@@ -329,12 +367,11 @@ int run_queries(frnn_engine* e, const BuiltGrid& b, bool sep, const float* d_q, 
             ST_TRY(grow(&e->q_sorted_idx, &e->q_sorted_bytes, (size_t)M, "allocating query order"));
             ST_TRY(grow(&e->q_inv, &e->q_inv_bytes, (size_t)M, "allocating query positions"));
             ST_TRY(grow(&e->q_start, &e->q_start_bytes, (size_t)cells + 1, "allocating query cell starts"));
-            ST_TRY(launch_status(frnn::launch_fill_i32(e->cnt, cells + 1, 0, s), "zero-fill query cells"));
+            ST_TRY(clean_counts(e, cells + 1));
             ST_TRY(launch_status(frnn::launch_bin_count(d_q, M, plan.grid_dim, plan.res, plan.inv_cell, frame,
                                                         (int)cells, e->q_cell_of, e->q_rank, e->cnt, s),
                                  "query bin/count launch"));
-            ST_TRY(launch_status(frnn::launch_exclusive_scan(e->cnt, (int)cells + 1, e->q_start, e->partials, s),
-                                 "query scan launch"));
+            ST_TRY(count_scan(e, cells, frame, e->q_start));
             ST_TRY(launch_status(frnn::launch_reorder(d_q, M, dim, e->q_cell_of, e->q_rank, e->q_start,
                                                       e->q_sorted_idx, e->q_inv, e->q_aos, e->stats_ws, q_frows,
                                                       s),
@@ -664,6 +701,13 @@ int frnn_engine_stage_times(const frnn_engine_t* e, float* ms, int n) {
 int frnn_engine_counters(const frnn_engine_t* e, long long* out, int n) {
     if (!e || !out) return fail(FRNN_ERR_INVALID_ARGUMENT, "null pointer");
     for (int i = 0; i < n && i < FRNN_NUM_COUNTERS; ++i) out[i] = e->ctr[i];
+    return FRNN_OK;
+}
+
+int frnn_engine_count_work(const frnn_engine_t* e, long long* out, int n) {
+    if (!e || !out) return fail(FRNN_ERR_INVALID_ARGUMENT, "null pointer");
+    const long long w[2] = {e->last_fill, e->last_scan > 0 ? (long long)e->status_host[4] + 1 : 0};
+    for (int i = 0; i < n && i < 2; ++i) out[i] = w[i];
     return FRNN_OK;
 }
 

@@ -133,6 +133,10 @@ int launch_fill_i32(int* p, long long n, int v, hipStream_t s);
 int launch_bin_count(const float* pts, int N, int g, int res, float inv_cell, const void* frame_ws,
                      int cells, int* cell_of, int* rank, int* cnt, hipStream_t s);
 int launch_exclusive_scan(const int* in, int n, int* out, int* partials, hipStream_t s);
+// The engine's scan of its count array: over min(n, *bound + 1) entries when
+// bound (a device int, the frame's cell count) is given, else n; the counts
+// are zeroed as they are read, so the array is clean for the next binning.
+int launch_count_scan(int* cnt, int n, const int* bound, int* out, int* partials, hipStream_t s);
 // The same scan with its partial sums in a file-scope device scratch array
 // (no workspace argument, no allocation); n <= scan_noalloc_max().  Returns
 // 0, 2 (n too large), 3 (launch error) or 4 (the scratch's device address

@@ -128,6 +128,7 @@ def _load():
         "frnn_engine_set_profiling": ([vp, i32], i32),
         "frnn_engine_stage_times": ([vp, vp, i32], i32),
         "frnn_engine_counters": ([vp, vp, i32], i32),
+        "frnn_engine_count_work": ([vp, vp, i32], i32),
         "frnn_grid_cells": ([i32, i32, ctypes.POINTER(_Plan)], i64),
         "frnn_launch_bin_count": ([vp, i32, i32, i32, f32, i64, vp, vp, vp, vp, vp], i32),
         "frnn_launch_exclusive_scan": ([vp, i32, vp, vp, vp], i32),
@@ -336,6 +337,15 @@ class FRNNEngine:
                                             NUM_COUNTERS), "counters")
         return {"shell_candidates": int(c[0]), "filter_hits": int(c[1]), "accepted": int(c[2]),
                 "streamed_pairs": int(c[3])}
+
+    @_serialised
+    def count_work(self):
+        """Count-array entries the last build zero-filled and scanned (the scan's
+        extent is a frame's actual cells + 1 when profiling events are on)."""
+        c = np.zeros(2, dtype=np.int64)
+        _check(_load().frnn_engine_count_work(self._handle(), c.ctypes.data_as(ctypes.c_void_p), 2),
+               "count_work")
+        return {"zero_filled": int(c[0]), "scanned": int(c[1])}
 
     @_serialised
     def close(self):
