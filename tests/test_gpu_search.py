@@ -279,6 +279,34 @@ def test_profiling_counters_and_stage_times():
     eng.close()
 
 
+def test_count_array_reuse_across_grids():
+    # the count scan zeroes the counts it reads, so only the first build on an
+    # engine fills the array; grids of different sizes and kinds in turn on
+    # one engine (projected frame, raw frame, a larger projected frame, the
+    # first again) must each match the oracle
+    eng = frnn_cuda.FRNNEngine(max_points=30000)
+    cases = [(unit_cloud(20000, 16, 4, 31), 32, 0.15), (unit_cloud(30000, 3, 3, 32), 16, 0.03),
+             (unit_cloud(30000, 12, 3, 33), 32, 0.1), (unit_cloud(20000, 16, 4, 31), 32, 0.15)]
+    eng.set_profiling(True, counters=False)
+    for j, (X, K, r) in enumerate(cases):
+        N, D = X.shape
+        d = device_soa(X)
+        eng.search_gpu(d.data_ptr(), N, D, K, r)
+        cw = eng.count_work()
+        log(f"count reuse {j}: D={D} N={N} plan={eng.last_plan()['path']} {cw}")
+        assert eng.last_plan()["path"] != "bruteforce"
+        assert cw["scanned"] >= 2
+        if j == 0:
+            assert cw["zero_filled"] >= cw["scanned"]
+        gi, gd = eng.get_results_numpy(N, K)
+        ri, rd = O.search(X, K, r)
+        assert_rows_equal(gi.reshape(K, N).T, gd.reshape(K, N).T, ri, rd, f"count reuse {j}")
+    # the same grid again: nothing left to fill
+    eng.search_gpu(d.data_ptr(), N, D, K, r)
+    assert eng.count_work()["zero_filled"] == 0
+    eng.close()
+
+
 @pytest.mark.parametrize("bad", ["nan", "inf"])
 def test_nonfinite_points_on_a_framed_grid(bad):
     # NaN: projections of such points are NaN (binned to cell 0, never within
