@@ -676,6 +676,32 @@ void search_kernel(SearchArgs a) {
         lsync();
         return true;
     };
+    // Final selection of two lists of at most 32 keys each (K <= 32), one per
+    // half of the wave: query q1's keys in lanes 0..31, q2's (q2 < 0: none)
+    // in lanes 32..63, ~0 filling both.  The network's first four levels sort
+    // blocks of 16 in alternating directions; the fifth merges each half
+    // ascending (direction of element bit 6, clear for every lane), so one
+    // 15-stage sort serves both queries.
+    auto final_pair = [&](int q1, int q2) __attribute__((always_inline)) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        const int c1 = min(s_cnt[q1], a.room);
+        const int c2 = q2 >= 0 ? min(s_cnt[q2], a.room) : 0;
+        const int qq = lower_half() ? q1 : q2;
+        const int cq = lower_half() ? c1 : c2;
+        const int i = lane & 31;
+        unsigned long long* L = lists + (size_t)(qq >= 0 ? qq : 0) * a.cap;
+        unsigned long long x[1];
+        x[0] = (qq >= 0 && i < cq) ? L[i] : ~0ull;
+#pragma unroll
+        for (int lk = 1; lk <= 4; ++lk) {
+#pragma unroll
+            for (int lj = lk - 1; lj >= 0; --lj) bitonic_step<1>(x, 1 << lk, 1 << lj);
+        }
+#pragma unroll
+        for (int lj = 4; lj >= 0; --lj) bitonic_step<1>(x, kWave, 1 << lj);
+        if (qq >= 0 && i < a.K) L[i] = i < cq ? x[0] : make_key(a.r2, -1);
+        lsync();
+    };
     auto select_topk = [&](int qn, bool final_pass) __attribute__((always_inline)) {
         // (lists whose new keys fit one register take the general path: the
         // same single sort without the staging)
@@ -727,6 +753,18 @@ void search_kernel(SearchArgs a) {
         const bool need = lower_half() && (final_pass ? lane < nq : s_cnt[lane] > a.room - kBatch);
         unsigned long long m = __ballot(need);
         if (m) {
+            if (final_pass && a.K <= 32) {
+                // lists of at most 32 keys: two per sort
+                unsigned long long sm = __ballot(need && min(s_cnt[n], a.room) <= 32);
+                m &= ~sm;
+                while (sm) {
+                    const int q1 = __ffsll((long long)sm) - 1;
+                    sm &= sm - 1;
+                    const int q2 = sm ? __ffsll((long long)sm) - 1 : -1;
+                    if (sm) sm &= sm - 1;
+                    final_pair(q1, q2);
+                }
+            }
             while (m) {
                 const int qn = __ffsll((long long)m) - 1;
                 m &= m - 1;
