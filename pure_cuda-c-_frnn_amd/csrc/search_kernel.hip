@@ -676,29 +676,30 @@ void search_kernel(SearchArgs a) {
         lsync();
         return true;
     };
-    // Final selection of two lists of at most 32 keys each (K <= 32), one per
-    // half of the wave: query q1's keys in lanes 0..31, q2's (q2 < 0: none)
-    // in lanes 32..63, ~0 filling both.  The network's first four levels sort
-    // blocks of 16 in alternating directions; the fifth merges each half
-    // ascending (direction of element bit 6, clear for every lane), so one
-    // 15-stage sort serves both queries.
-    auto final_pair = [&](int q1, int q2) __attribute__((always_inline)) {
+    // Final selection of 64 / W lists of at most W keys each (W = 16 or 32,
+    // K <= W), one per W-lane block of the wave: query qs[g]'s keys in block
+    // g (qs[g] < 0: none), ~0 filling the rest.  The network's first levels
+    // sort blocks of W / 2 in alternating directions; the last merges each
+    // block ascending (the direction of element bit 6, clear for every lane),
+    // so one sort of log2(W) levels (10 or 15 stages) serves them all.
+    auto final_group = [&](auto lw_const, const int (&qs)[4]) __attribute__((always_inline)) {
+        constexpr int LW = decltype(lw_const)::value;   // log2(W)
+        constexpr int W = 1 << LW;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        const int c1 = min(s_cnt[q1], a.room);
-        const int c2 = q2 >= 0 ? min(s_cnt[q2], a.room) : 0;
-        const int qq = lower_half() ? q1 : q2;
-        const int cq = lower_half() ? c1 : c2;
-        const int i = lane & 31;
+        const int g = lane >> LW;
+        const int qq = g == 0 ? qs[0] : g == 1 ? qs[1] : g == 2 ? qs[2] : qs[3];
+        const int cq = qq >= 0 ? min(s_cnt[qq], a.room) : 0;
+        const int i = lane & (W - 1);
         unsigned long long* L = lists + (size_t)(qq >= 0 ? qq : 0) * a.cap;
         unsigned long long x[1];
-        x[0] = (qq >= 0 && i < cq) ? L[i] : ~0ull;
+        x[0] = i < cq ? L[i] : ~0ull;
 #pragma unroll
-        for (int lk = 1; lk <= 4; ++lk) {
+        for (int lk = 1; lk < LW; ++lk) {
 #pragma unroll
             for (int lj = lk - 1; lj >= 0; --lj) bitonic_step<1>(x, 1 << lk, 1 << lj);
         }
 #pragma unroll
-        for (int lj = 4; lj >= 0; --lj) bitonic_step<1>(x, kWave, 1 << lj);
+        for (int lj = LW - 1; lj >= 0; --lj) bitonic_step<1>(x, kWave, 1 << lj);
         if (qq >= 0 && i < a.K) L[i] = i < cq ? x[0] : make_key(a.r2, -1);
         lsync();
     };
@@ -754,15 +755,33 @@ void search_kernel(SearchArgs a) {
         unsigned long long m = __ballot(need);
         if (m) {
             if (final_pass && a.K <= 32) {
-                // lists of at most 32 keys: two per sort
-                unsigned long long sm = __ballot(need && min(s_cnt[n], a.room) <= 32);
-                m &= ~sm;
-                while (sm) {
-                    const int q1 = __ffsll((long long)sm) - 1;
+                // lists of at most 16 keys (K <= 16): four per sort; of at
+                // most 32: two per sort
+                const int cn = min(s_cnt[n], a.room);
+                auto take = [&](unsigned long long& sm) __attribute__((always_inline)) -> int {
+                    if (!sm) return -1;
+                    const int q = __ffsll((long long)sm) - 1;
                     sm &= sm - 1;
-                    const int q2 = sm ? __ffsll((long long)sm) - 1 : -1;
-                    if (sm) sm &= sm - 1;
-                    final_pair(q1, q2);
+                    return q;
+                };
+                if (a.K <= 16) {
+                    unsigned long long s16 = __ballot(need && cn <= 16);
+                    m &= ~s16;
+                    while (s16) {
+                        int qs[4];
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) qs[g] = take(s16);
+                        final_group(IntC<4>{}, qs);
+                    }
+                }
+                unsigned long long s32 = __ballot(need && cn <= 32) & m;
+                m &= ~s32;
+                while (s32) {
+                    int qs[4];
+                    qs[0] = take(s32);
+                    qs[1] = take(s32);
+                    qs[2] = qs[3] = -1;
+                    final_group(IntC<5>{}, qs);
                 }
             }
             while (m) {
