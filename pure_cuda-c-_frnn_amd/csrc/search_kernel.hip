@@ -1530,7 +1530,10 @@ static void launch_ds(const SearchArgs& a, bool bf, hipStream_t s) {
 // rounds of the device's resident workgroups; with too few blocks for the last
 // round, most of the device idles through it.  Splitting the points into S
 // ranges gives S times as many shorter workgroups: S is the smallest count
-// (at most 8) whose last round is at least 90% full, else the fullest.
+// (at most 8) whose rounds are at least 97% full, else the fullest.  Each
+// range keeps its own K keys per query (more accepted keys, one more merge
+// step per range), which the fuller rounds outweigh: C5 (1 563 workgroups, 512
+// resident) 104.0 ms at S = 3 (92% full), 101.7 at S = 5 (95%), 101.2 at S = 7.
 static int resident_bf_blocks(int DS) {
     static int cached[2] = {0, 0};
     const int k = DS >= 128 ? 1 : 0;
@@ -1564,7 +1567,7 @@ int search_ranges(const frnn_plan_t& plan, int D, int N, int M) {
         const long long units = blocks * S;
         const long long rounds = (units + slots - 1) / slots;
         const double fill = (double)units / (double)(rounds * slots);
-        if (fill >= 0.9) return S;
+        if (fill >= 0.97) return S;
         if (fill > best_fill + 1e-9) {
             best_fill = fill;
             best = S;
