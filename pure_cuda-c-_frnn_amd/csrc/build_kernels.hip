@@ -11,8 +11,10 @@
 //   * the reorder writes one padded AoS row per point (stride roundup(D,4)),
 //     i.e. 16-byte-aligned vector stores of whole rows instead of D scattered
 //     4-byte stores into SoA planes, and also records the inverse permutation;
-//   * the scan is a three-phase reduce/scan/propagate over 4096-element tiles
-//     (16-byte coalesced accesses) with no inter-block spin waits.
+//   * the scan is two passes over 4096-element tiles (16-byte coalesced
+//     accesses) with no inter-block spin waits: a reduce writes each tile's
+//     sum, then each tile adds the earlier tiles' sums (from L2) to its own
+//     block scan.
 #include <mutex>
 
 #include "frnn_device.hpp"
@@ -132,27 +134,6 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const int* __
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
 
-// Single block: exclusive scan of up to kScanTile partial sums, in place.
-__global__ __launch_bounds__(kScanThreads) void scan_partials_kernel(int* __restrict__ partials, int nb) {
-    __shared__ int s_w[kScanThreads / kWave];
-    constexpr int kPer = kScanTile / kScanThreads;
-    const int base = threadIdx.x * kPer;
-    int v[kPer];
-    int sum = 0;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        v[j] = (base + j < nb) ? partials[base + j] : 0;
-        sum += v[j];
-    }
-    int total;
-    int run = block_exclusive_scan_256(sum, s_w, &total);
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        if (base + j < nb) partials[base + j] = run;
-        run += v[j];
-    }
-}
-
 // CLEAR: the input entries are zeroed once read (the count array starts the
 // next binning clean, with no separate fill).
 template <bool VEC, bool CLEAR>
@@ -170,7 +151,12 @@ __global__ __launch_bounds__(kScanThreads) void scan_final_kernel(int* __restric
 #pragma unroll
         for (int j = 0; j < kScanRows; ++j) scan_store4<VEC>(in, base + j * 4 * kScanThreads, n, make_int4(0, 0, 0, 0));
     }
-    int carry = partials[blockIdx.x];
+    // the tile's carry: the sum of the earlier tiles' partial sums (at most
+    // kScanTile of them, read from L2 while this tile's loads are in flight)
+    int pre = 0;
+    for (int k = threadIdx.x; k < (int)blockIdx.x; k += kScanThreads) pre += partials[k];
+    int carry;
+    block_exclusive_scan_256(pre, s_w, &carry);
 #pragma unroll
     for (int j = 0; j < kScanRows; ++j) {
         int total;
@@ -978,7 +964,7 @@ int scan_partials_count(int n) { return (n + kScanTile - 1) / kScanTile + 1; }
 // (with that device current, on its first call) and used for every kernel
 // argument.  Every call on one device shares the array: calls that overlap on
 // a device race.  Nothing in it needs clearing: the reduce pass writes every
-// partial the later passes read.
+// partial the final pass reads.
 static __device__ __align__(256) int scratch[kScanTile];
 
 namespace {
@@ -1030,7 +1016,6 @@ int scan_launch(const int* in, int n, int* out, int* partials, const int* bound,
         hipLaunchKernelGGL(scan_reduce_kernel<true>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, bound);
     else
         hipLaunchKernelGGL(scan_reduce_kernel<false>, dim3(nb), dim3(kScanThreads), 0, s, in, n, partials, bound);
-    hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(kScanThreads), 0, s, partials, nb);
     if (vec)
         hipLaunchKernelGGL((scan_final_kernel<true, CLEAR>), dim3(nb), dim3(kScanThreads), 0, s, io, n, partials,
                            out, bound);
