@@ -3,7 +3,9 @@
 Bar: bit-exact neighbour indices, counts and distances on every compared row
 (rows are the K smallest (d2, idx) keys in ascending order, padded (r2, -1)).
 Full-size BASELINE configs are checked on sampled queries against the oracle
-run over the full database, plus size-independent row properties.
+run over the full database, plus size-independent row properties; C1, C2 and
+C3 on every row at full size, the metric workload on every row at 300 000
+points.
 """
 import glob
 import os
@@ -381,6 +383,20 @@ def test_baseline_configs_all_rows(name):
     assert plan["path"] == "grid_full"
     ri, rd = O.search(w.X, w.K, w.radius)
     assert_rows_equal(gi, gd, ri, rd, f"{name} all rows")
+
+
+@pytest.mark.parametrize("name,N", [("metric", 300_000), ("C3", 500_000)])
+def test_framed_configs_all_rows(name, N):
+    """Every row of the projected-frame searches (rows of 16 and 12 floats):
+    C3 at full size and the metric workload at 300 000 points (its radius
+    follows N), against the oracle's first-coordinate grid over the full
+    database."""
+    w = W.config(name, N=N)
+    log(f"all rows {name}: N={w.N} D={w.D} K={w.K} r={w.radius:.6f}")
+    gi, gd, plan = engine_search(w.X, w.K, w.radius)
+    assert plan["path"] == "grid_first"
+    ri, rd = O.search(w.X, w.K, w.radius)
+    assert_rows_equal(gi, gd, ri, rd, f"{name} N={N} all rows")
 
 
 @pytest.mark.parametrize("D,k,N,r,K", [(64, 4, 1500, 0.6, 32), (128, 4, 1200, 0.8, 128), (40, 4, 1000, 0.5, 16)])
