@@ -212,15 +212,16 @@ __device__ __forceinline__ float exact_d2(const float* q, const float* __restric
     return acc;
 }
 
-// Rows of up to 12 floats keep five waves per SIMD resident (register budget
-// 96), rows of 16 four (128): the search is bound by the latency of its
-// gathers, list round trips and sorts, so the extra wave outweighs a few
-// spilled registers (measured: DS = 4 and 12 fastest at five, DS = 8 the same
-// at four or five; at DS = 16 the compiler cannot fit five).
+// Rows of 4 floats keep six waves per SIMD resident (register budget 80),
+// rows of 8 and 12 five (96), rows of 16 four (128): the search is bound by
+// the latency of its gathers, list round trips and sorts, so the extra wave
+// outweighs a few spilled registers (measured: DS = 4 about 1% faster at six
+// than at five, DS = 12 fastest at five, DS = 8 the same at four or five; at
+// DS = 16 the compiler cannot fit five).
 // Larger rows keep two (256 VGPRs + AGPRs), so a second wave's MFMA chain can
 // overlap one wave's hit handling.
 template <int DS>
-struct WavesPerEU { static constexpr int value = DS <= 12 ? 5 : DS <= 16 ? 4 : 2; };
+struct WavesPerEU { static constexpr int value = DS <= 4 ? 6 : DS <= 12 ? 5 : DS <= 16 ? 4 : 2; };
 
 // CNT: the profiling build of the kernel, which also keeps the work counters
 // (a separate instantiation, so the counting code costs the plain kernel no
