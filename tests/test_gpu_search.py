@@ -144,6 +144,23 @@ def test_reference_sweep_cell_sampled():
     assert_rows_equal(gi[q], gd[q], ri, rd, "refD16N200000 sampled")
 
 
+@pytest.mark.parametrize("D,N,r,K", [(3, 200_000, 0.004, 32), (2, 60_000, 0.0005, 16)])
+def test_bruteforce_rows_of_4_at_scale(D, N, r, K):
+    # radii below the grid's cell limit send D <= 4 to brute force (rows of 4
+    # floats): a dense cluster gives the lists K-deep neighbourhoods, and a
+    # run of duplicates gives exact ties; more chunks than fit the device at
+    # once, every row against the oracle
+    rs = np.random.RandomState(8 + D)
+    X = (0.5 + 0.01 * rs.randn(N, D)).astype(np.float32)
+    X[100:140] = X[0]
+    log(f"bruteforce rows of 4: N={N} D={D} K={K} r={r}")
+    gi, gd, plan = engine_search(X, K, r)
+    assert plan["path"] == "bruteforce"
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, f"bruteforce D={D} N={N}")
+    assert (ri >= 0).sum(1).mean() > K / 2
+
+
 def test_nan_points_have_no_neighbours():
     rs = np.random.RandomState(6)
     X = rs.rand(2000, 16).astype(np.float32)
