@@ -161,6 +161,21 @@ def test_bruteforce_rows_of_4_at_scale(D, N, r, K):
     assert (ri >= 0).sum(1).mean() > K / 2
 
 
+@pytest.mark.parametrize("D,k,N,r,K,path", [(5, 5, 100_000, 0.1, 16, "grid_full"),
+                                             (8, 3, 100_000, 0.05, 32, "grid_first"),
+                                             (7, 3, 150_000, 0.05, 16, "grid_first")])
+def test_rows_of_8_at_scale(D, k, N, r, K, path):
+    # rows padded to 8 floats (D = 5..8) on a full-D grid and on projected
+    # frames, every row against the oracle
+    X = unit_cloud(N, D, k, 13)
+    X[7] = X[3]
+    log(f"rows of 8: N={N} D={D} K={K} r={r} {path}")
+    gi, gd, plan = engine_search(X, K, r)
+    assert plan["path"] == path
+    ri, rd = O.search(X, K, r)
+    assert_rows_equal(gi, gd, ri, rd, f"rows of 8 D={D} N={N}")
+
+
 def test_nan_points_have_no_neighbours():
     rs = np.random.RandomState(6)
     X = rs.rand(2000, 16).astype(np.float32)
