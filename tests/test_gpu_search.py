@@ -163,17 +163,20 @@ def test_bruteforce_rows_of_4_at_scale(D, N, r, K):
 
 @pytest.mark.parametrize("D,k,N,r,K,path", [(5, 5, 100_000, 0.1, 16, "grid_full"),
                                              (8, 3, 100_000, 0.05, 32, "grid_first"),
-                                             (7, 3, 150_000, 0.05, 16, "grid_first")])
-def test_rows_of_8_at_scale(D, k, N, r, K, path):
+                                             (7, 3, 150_000, 0.05, 16, "grid_first"),
+                                             (24, 3, 60_000, 0.1, 32, "grid_first"),
+                                             (32, 4, 60_000, 0.15, 16, "grid_first")])
+def test_rows_of_8_and_32_at_scale(D, k, N, r, K, path):
     # rows padded to 8 floats (D = 5..8) on a full-D grid and on projected
-    # frames, every row against the oracle
+    # frames, and rows of 32 floats (D = 17..32) on projected frames, every
+    # row against the oracle
     X = unit_cloud(N, D, k, 13)
     X[7] = X[3]
-    log(f"rows of 8: N={N} D={D} K={K} r={r} {path}")
+    log(f"rows at scale: N={N} D={D} K={K} r={r} {path}")
     gi, gd, plan = engine_search(X, K, r)
     assert plan["path"] == path
     ri, rd = O.search(X, K, r)
-    assert_rows_equal(gi, gd, ri, rd, f"rows of 8 D={D} N={N}")
+    assert_rows_equal(gi, gd, ri, rd, f"rows at scale D={D} N={N}")
 
 
 def test_nan_points_have_no_neighbours():
