@@ -165,11 +165,13 @@ def test_bruteforce_rows_of_4_at_scale(D, N, r, K):
                                              (8, 3, 100_000, 0.05, 32, "grid_first"),
                                              (7, 3, 150_000, 0.05, 16, "grid_first"),
                                              (24, 3, 60_000, 0.1, 32, "grid_first"),
-                                             (32, 4, 60_000, 0.15, 16, "grid_first")])
-def test_rows_of_8_and_32_at_scale(D, k, N, r, K, path):
+                                             (32, 4, 60_000, 0.15, 16, "grid_first"),
+                                             (48, 3, 40_000, 0.15, 16, "grid_first"),
+                                             (64, 4, 40_000, 0.2, 32, "grid_first")])
+def test_rows_of_8_to_64_at_scale(D, k, N, r, K, path):
     # rows padded to 8 floats (D = 5..8) on a full-D grid and on projected
-    # frames, and rows of 32 floats (D = 17..32) on projected frames, every
-    # row against the oracle
+    # frames, rows of 32 and 64 floats (D = 17..64) on projected frames,
+    # every row against the oracle
     X = unit_cloud(N, D, k, 13)
     X[7] = X[3]
     log(f"rows at scale: N={N} D={D} K={K} r={r} {path}")
